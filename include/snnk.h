@@ -1,0 +1,98 @@
+/*
+ * snnk.h -- C ABI of libsnnk, the MI355X (gfx950) spiking-neural-network
+ * inference kernel library.
+ *
+ * Every entry point follows the same contract:
+ *   - returns int: 0 = ok, negative = invalid argument / unsupported
+ *     configuration (see SNNK_E*), positive = the hipError_t raised by the
+ *     launch;
+ *   - takes the HIP stream (hipStream_t, passed as void*) and only enqueues
+ *     work on it: no synchronisation, no host<->device copies;
+ *   - never allocates: every buffer is owned by the caller and passed as a
+ *     raw device pointer;
+ *   - sizes are int64_t; tensors are dense row-major in the layout stated;
+ *   - is re-entrant and thread-safe (no mutable global state).
+ *
+ * The reference operator each entry point replaces is cited as
+ * path:line inside Xarlley/Triton-Pass-Analysis.
+ */
+#ifndef SNNK_H_
+#define SNNK_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define SNNK_OK            0
+#define SNNK_EINVAL       -1   /* bad pointer / size / enum value          */
+#define SNNK_EUNSUPPORTED -2   /* valid request this build does not cover   */
+#define SNNK_EALIGN       -3   /* pointer alignment the kernel requires      */
+
+/* ---- element types --------------------------------------------------- */
+#define SNNK_F32   0
+#define SNNK_BF16  1
+#define SNNK_F16   2
+#define SNNK_U8    3
+#define SNNK_I32   4
+
+/* ---- spike output formats ------------------------------------------- */
+#define SNNK_SPIKE_SAME  0   /* 0/1 in the input's element type            */
+#define SNNK_SPIKE_U8    1   /* 0/1 as uint8                                */
+
+/* ---- threshold modes (snn_compiler/kernels/neurons.py:66-68) --------- */
+#define SNNK_THR_SCALAR      0
+#define SNNK_THR_PER_CHANNEL 1
+#define SNNK_THR_PER_NEURON  2
+
+/* Library version (major*10000 + minor*100 + patch). */
+int snnk_version(void);
+
+/* Human-readable text for a status code returned by any entry point. */
+const char* snnk_status_string(int status);
+
+/*
+ * Multi-step IF/LIF neuron, optionally fused with a per-channel bias, a
+ * residual input, an initial / final membrane state and a spike-count
+ * (rate) output.
+ *
+ * Replaces:
+ *   if_lif                      snn_compiler/kernels/neurons.py:311-376
+ *   fused_bias_if_lif           snn_compiler/kernels/fused.py:117-226
+ *   fused_bias_if_lif_rate      snn_compiler/kernels/fused.py:303-382
+ *   fused_bias_if_lif_stateful  snn_compiler/kernels/fused.py:444-507
+ *
+ * x        [T, NCL] elements of x_dtype (F32/BF16/F16); NCL = B*C*H*W
+ * bias     [C] float or NULL; channel of flat index i is (i/HW)%C, or i%C
+ *          when channel_last != 0
+ * residual [T, NCL] of x_dtype or NULL
+ * vth      [C] (PER_CHANNEL) or [NCL] (PER_NEURON) float; unused if SCALAR
+ * v_init   [NCL] float or NULL (state starts at 0)
+ * v_out    [NCL] float or NULL: membrane state after the last step
+ * spikes   [T, NCL] in spike_fmt, or NULL (only count_out wanted)
+ * count_out[NCL] float or NULL: sum over T of the spikes
+ *
+ * Per element and step t (all arithmetic fp32, rounded after every
+ * operation, no fused multiply-add):
+ *     u = x_t (+ bias[c]) (+ residual_t)
+ *     v = decay*v + in_scale*u
+ *     s = v >= threshold
+ *     hard reset: v = s ? v_reset : v;  soft reset: v = s ? v - threshold : v
+ */
+int snnk_lif_forward(const void* x, int32_t x_dtype,
+                     const float* bias, const void* residual,
+                     const float* vth, int32_t thr_mode, float vth_scalar,
+                     const float* v_init, float* v_out,
+                     void* spikes, int32_t spike_fmt, float* count_out,
+                     int64_t T, int64_t NCL, int64_t C, int64_t HW,
+                     int32_t channel_last,
+                     float decay, float in_scale, float v_reset,
+                     int32_t soft_reset, void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* SNNK_H_ */

@@ -1,0 +1,109 @@
+"""ctypes boundary to libsnnk.so.
+
+The library exposes a plain C ABI (``include/snnk.h``): raw device pointers,
+int64 sizes, an ``int`` status and the HIP stream as ``void*``.  This module
+loads it, declares every prototype once, and turns a non-zero status into a
+Python exception.  It never falls back to another implementation: if the
+library is missing the first call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+import threading
+
+import torch
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "libsnnk.so"
+
+# status codes (include/snnk.h)
+OK, EINVAL, EUNSUPPORTED, EALIGN = 0, -1, -2, -3
+# element types
+F32, BF16, F16, U8, I32 = 0, 1, 2, 3, 4
+# spike formats
+SPIKE_SAME, SPIKE_U8 = 0, 1
+# threshold modes
+THR_SCALAR, THR_PER_CHANNEL, THR_PER_NEURON = 0, 1, 2
+
+_p = C.c_void_p
+_i32 = C.c_int32
+_i64 = C.c_int64
+_f32 = C.c_float
+
+# name -> argtypes (restype is int for every entry point except the two
+# informational ones declared below).
+PROTOTYPES: dict[str, list] = {
+    "snnk_lif_forward": [
+        _p, _i32,              # x, x_dtype
+        _p, _p,                # bias, residual
+        _p, _i32, _f32,        # vth, thr_mode, vth_scalar
+        _p, _p,                # v_init, v_out
+        _p, _i32, _p,          # spikes, spike_fmt, count_out
+        _i64, _i64, _i64, _i64,  # T, NCL, C, HW
+        _i32,                  # channel_last
+        _f32, _f32, _f32,      # decay, in_scale, v_reset
+        _i32, _p,              # soft_reset, stream
+    ],
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class SnnkError(RuntimeError):
+    """A libsnnk entry point returned a non-zero status."""
+
+
+def lib():
+    """Load libsnnk.so once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m snnk.build` "
+                "(or __graft_entry__.build()); snnk has no fallback path")
+        h = C.CDLL(str(LIB_PATH))
+        h.snnk_version.restype = C.c_int
+        h.snnk_version.argtypes = []
+        h.snnk_status_string.restype = C.c_char_p
+        h.snnk_status_string.argtypes = [C.c_int]
+        for name, argtypes in PROTOTYPES.items():
+            fn = getattr(h, name)
+            fn.restype = C.c_int
+            fn.argtypes = argtypes
+        _lib = h
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        msg = lib().snnk_status_string(status).decode()
+        raise SnnkError(f"{what}: libsnnk status {status} ({msg})")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream(device: torch.device | None = None) -> int:
+    """The current torch stream on ``device`` as a raw hipStream_t."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+_DT = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16,
+       torch.uint8: U8, torch.int32: I32}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DT[dt]
+    except KeyError:
+        raise AssertionError(f"unsupported dtype {dt}") from None
