@@ -8,12 +8,12 @@ the operator over one batch of synthetic, seeded input that is resident in HBM
 before timing starts.  Buffers rotate over several sets (> 512 MiB in total)
 so that the 256 MiB MALL cannot serve a step from the previous step's data.
 
-Two timed passes per workload:
-  * whole job: K steps captured in a HIP graph and replayed, bracketed by
-    torch.cuda.synchronize() -> ms_per_step and ``value``;
-  * per kernel: K eager launches, each bracketed by a pair of HIP events on
-    the launch stream -> the dominant kernel's average duration, from which
-    ``roofline.achieved`` = algorithmic bytes (or ops) per launch / duration.
+Timing: K steps are captured in a HIP graph and replayed; the replay is
+bracketed by torch.cuda.synchronize() (wall clock -> ms_per_step, ``value``)
+and by two HIP events on the launch stream.  For workloads whose step has
+several kernels the dominant kernel is captured and replayed on its own the
+same way.  ``roofline.achieved`` = algorithmic bytes (or ops) per launch of
+the dominant kernel / its event-timed average duration.
 The CPU baseline times the oracle (a restatement of the reference's PyTorch CPU
 path) on the host cores on a bounded sample and reports it beside the GPU
 figure.  One JSON line is printed.
@@ -63,39 +63,52 @@ def time_cpu(fn, budget_s: float = 8.0, min_runs: int = 3) -> float:
     return statistics.median(times)
 
 
-def time_gpu(step, nsets: int, steps: int, warmup: int):
-    """(wall seconds per step via graph replay, mean per-launch event ms)."""
+def _graph_of(fn, steps: int, nsets: int):
+    """Capture ``steps`` launches of fn(i % nsets) into one HIP graph."""
     stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        step(i % nsets)
-    torch.cuda.synchronize()
-    # per-launch kernel durations (eager, HIP events on the launch stream)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
-    for i in range(steps):
-        ev[i][0].record(stream)
-        step(i % nsets)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    kern_ms = [a.elapsed_time(b) for a, b in ev]
-    # whole job: the K steps captured once, replayed
     graph = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream()
     cap.wait_stream(stream)
     with torch.cuda.stream(cap):
-        step(0)  # one eager launch on the capture stream before capture
+        fn(0)  # one eager launch on the capture stream before capture
         with torch.cuda.graph(graph, stream=cap):
             for i in range(steps):
-                step(i % nsets)
+                fn(i % nsets)
     stream.wait_stream(cap)
     torch.cuda.synchronize()
-    graph.replay()
+    return graph
+
+
+def time_gpu(step, nsets: int, steps: int, warmup: int, kernel=None):
+    """Time ``steps`` launches of ``step`` (and of the dominant ``kernel``).
+
+    Returns (wall seconds per step, mean ms per dominant-kernel launch).  The
+    launches are captured once in a HIP graph; after a warm replay, the timed
+    replay is bracketed by torch.cuda.synchronize() for the wall clock and by
+    two HIP events on the launch stream for the kernel average.
+    """
+    for i in range(warmup):
+        step(i % nsets)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    graph.replay()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
-    return wall, statistics.mean(kern_ms), statistics.median(kern_ms)
+    stream = torch.cuda.current_stream()
+
+    def timed(fn):
+        g = _graph_of(fn, steps, nsets)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / steps
+        return wall, e0.elapsed_time(e1) / steps
+
+    wall, ev_ms = timed(step)
+    if kernel is not None:
+        _, ev_ms = timed(kernel)
+    return wall, ev_ms
 
 
 # --------------------------------------------------------------------------
@@ -119,7 +132,7 @@ def bench_lif(args, dev):
         launch_lif(xs[i], thr=(THR_SCALAR, None, 1.0), spikes=ss[i], v_out=vs[i],
                    C=C, HW=H * W, decay=0.5, in_scale=0.5, v_reset=0.0)
 
-    wall, kern_mean, kern_med = time_gpu(step, nsets, args.steps, args.warmup)
+    wall, kern_ms = time_gpu(step, nsets, args.steps, args.warmup)
     # parity of what the timed graph wrote
     s_ref, v_ref, _ = on.lif_multistep(x_cpu, neuron="lif", tau=2.0)
     ok = torch.equal(ss[0].cpu(), s_ref) and torch.equal(vs[0].cpu(), v_ref)
@@ -132,11 +145,11 @@ def bench_lif(args, dev):
                    "reset": "hard0", "spike_dtype": "f32", "final_v": True,
                    "rotating_sets": nsets},
         "roofline": {"bound": "hbm", "kernel": "lif_kernel",
-                     "achieved": bytes_per / (kern_mean * 1e-3) / 1e9,
+                     "achieved": bytes_per / (kern_ms * 1e-3) / 1e9,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": bytes_per / (kern_mean * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "frac": bytes_per / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                      "traffic": None, "algorithmic_bytes": bytes_per,
-                     "kernel_ms_mean": kern_mean, "kernel_ms_median": kern_med},
+                     "kernel_ms_mean": kern_ms},
         "parity": ok,
     }
     if not args.no_cpu_baseline:
@@ -151,8 +164,85 @@ def bench_lif(args, dev):
     return rec
 
 
-WORKLOADS = {"lif": bench_lif}
-HEADLINE_ORDER = ["lif"]
+# --------------------------------------------------------------------------
+# Bit-packed binary GEMM
+# --------------------------------------------------------------------------
+INT8_PEAK_TOPS = 5030.0
+
+
+def bench_bgemm(args, dev):
+    import numpy as np
+    import snnk
+    from snnk.kernels.binary import _gemm_packed
+    from oracle import bits as ob, clib
+
+    M, K, N = 8192, 4096, 4096
+    g = torch.Generator().manual_seed(0)
+    A = torch.rand(M, K, generator=g) < 0.1
+    W = torch.rand(K, N, generator=g) < 0.5
+    Ap = snnk.pack_bits(A.to(dev, torch.uint8))
+    Wp = snnk.pack_bits(W.to(dev, torch.uint8), dim=-2)
+    ops = 2.0 * M * N * K
+    set_bytes = Ap.numel() * 4 + Wp.numel() * 4 + M * N * 4
+    nsets = max(2, math.ceil(ROTATE_BYTES / set_bytes))
+    As = [Ap.clone() for _ in range(nsets)]
+    Ws = [Wp.clone() for _ in range(nsets)]
+    Cs = [torch.empty(M, N, device=dev, dtype=torch.int32) for _ in range(nsets)]
+
+    def step(i):
+        _gemm_packed(As[i], Ws[i], K, signed=False, algo="mfma", out_dtype=torch.int32,
+                     out=Cs[i])
+
+    wall, kern_ms = time_gpu(step, nsets, args.steps, args.warmup)
+    # parity: exact row sample vs the C oracle + exact row/column checksums
+    Cn = Cs[0].cpu().numpy().astype(np.int64)
+    A_np, W_np = A.numpy().astype(np.uint8), W.numpy().astype(np.uint8)
+    Ap_ref, Wp_ref = ob.pack_rows(A_np), ob.pack_rows(W_np.T)
+    ok = np.array_equal(Cn[:64], clib.popcount_gemm(Ap_ref, Wp_ref, rows=(0, 64)))
+    ok = ok and np.array_equal(Cn.sum(1), A_np.astype(np.int64) @ W_np.astype(np.int64).sum(1))
+    ok = ok and np.array_equal(Cn.sum(0), A_np.astype(np.int64).sum(0) @ W_np.astype(np.int64))
+
+    # one-off operand packing cost (activations would be packed per call)
+    A_u8 = A.to(dev, torch.uint8)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        snnk.pack_bits(A_u8, dim=-1)
+    e1.record()
+    torch.cuda.synchronize()
+    pack_ms = e0.elapsed_time(e1) / 20
+
+    achieved = ops / (kern_ms * 1e-3) / 1e12
+    rec = {
+        "workload": "bgemm", "value": ops / wall / 1e12, "unit": "TOPS",
+        "ms_per_step": wall * 1e3, "dtype": "u1 (bit-packed u32) x u1 -> i32",
+        "config": {"workload": "binary_gemm_M8192_K4096_N4096_packed_u32", "M": M, "K": K,
+                   "N": N, "p_A": 0.1, "p_W": 0.5, "signed": False, "algo": "mfma_i8",
+                   "rotating_sets": nsets},
+        "roofline": {"bound": "mfma", "kernel": "bgemm_mfma_kernel",
+                     "achieved": achieved, "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                     "frac": achieved / INT8_PEAK_TOPS, "traffic": None,
+                     "algorithmic_ops": ops, "kernel_ms_mean": kern_ms,
+                     "peak_note": "dense int8 MFMA (v_mfma_i32_32x32x32_i8)"},
+        "pack_A_ms": pack_ms,
+        "parity": bool(ok),
+    }
+    if not args.no_cpu_baseline:
+        torch.set_num_threads(cpu_threads())
+        Af, Wf = A.float(), W.float()
+        rows = 2048
+        sec = time_cpu(lambda: Af[:rows] @ Wf, budget_s=6.0)
+        rec["cpu_baseline"] = {"value": 2.0 * rows * N * K / sec / 1e12, "unit": "TOPS",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"exact fp32 matmul of the {{0,1}} operands "
+                                         f"(counts < 2^24), first {rows} of {M} rows",
+                               "seconds_per_call": sec}
+    return rec
+
+
+WORKLOADS = {"lif": bench_lif, "bgemm": bench_bgemm}
+HEADLINE_ORDER = ["lif", "bgemm"]
 
 
 def main():

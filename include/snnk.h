@@ -91,6 +91,48 @@ int snnk_lif_forward(const void* x, int32_t x_dtype,
                      float decay, float in_scale, float v_reset,
                      int32_t soft_reset, void* stream);
 
+/*
+ * Pack {0,1} elements into uint32 words along K: element k of a row becomes
+ * bit k%32 of word k/32 (least-significant first); bits past K are zero.
+ *
+ * Replaces:
+ *   _pack_N / _pack_N_kernel  snn_compiler/kernels/attention.py:195-214,236-242
+ *   bitpack_N (torch packer)  snn_compiler/explore/attention/phase6b_bitpack.py:35-46
+ *
+ * src  element (b, r, k) at src + b*stride_b + r*stride_r + k*stride_k
+ *      (strides in elements; src_dtype F32/BF16/F16/U8; nonzero -> 1)
+ * dst  [batch, rows, ceil(K/32)] uint32, dense
+ */
+int snnk_pack_bits(const void* src, int32_t src_dtype, uint32_t* dst,
+                   int64_t batch, int64_t rows, int64_t K,
+                   int64_t stride_b, int64_t stride_r, int64_t stride_k,
+                   void* stream);
+
+/* binary GEMM algorithms */
+#define SNNK_BGEMM_AUTO    0   /* MFMA when M, N, K >= 128, else POPC          */
+#define SNNK_BGEMM_POPC    1   /* VALU and + popcount-accumulate               */
+#define SNNK_BGEMM_MFMA_I8 2   /* bits expanded to int8, v_mfma_i32_32x32x32_i8 */
+
+/*
+ * Batched binary GEMM over bit-packed operands:
+ *   C[b][m][n] = sum_k A[b][m][k] * B[b][n][k]              (signed_w == 0)
+ *   C[b][m][n] = 2*sum_k A*B - sum_k A[b][m][k]              (signed_w != 0:
+ *                B bit 1 means weight +1, bit 0 means -1)
+ *
+ * Replaces (generalised): spike_ktv_popcount / _ktv_popcount_kernel
+ *   snn_compiler/kernels/attention.py:217-233,245-258
+ *
+ * A  [batch][M][lda] uint32 words (lda >= ceil(K/32)), B [batch][N][ldb],
+ * C  [batch][M][ldc] of c_dtype (I32, or F32 as the reference returns);
+ * strides between batch entries in words / elements (ignored if batch == 1).
+ * Bits past K in the last word are ignored.
+ */
+int snnk_binary_gemm(const uint32_t* A, const uint32_t* B, void* C, int32_t c_dtype,
+                     int64_t batch, int64_t M, int64_t N, int64_t K,
+                     int64_t lda, int64_t ldb, int64_t ldc,
+                     int64_t stride_a, int64_t stride_b, int64_t stride_c,
+                     int32_t signed_w, int32_t algo, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

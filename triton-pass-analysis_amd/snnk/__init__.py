@@ -7,13 +7,13 @@ backed by hand-written HIP kernels in ``libsnnk.so`` behind a C ABI
 missing raises.
 """
 from .kernels import (
-    if_lif,
+    if_lif, pack_bits, binary_gemm, spike_ktv_popcount, HAS_POPC,
     fused_bias_if_lif, fused_bias_if_lif_rate, fused_bias_if_lif_stateful,
     conv_neuron, linear_neuron, conv_bn_neuron, fold_conv_bn,
 )
 
 __all__ = [
-    "if_lif",
+    "if_lif", "pack_bits", "binary_gemm", "spike_ktv_popcount", "HAS_POPC",
     "fused_bias_if_lif", "fused_bias_if_lif_rate", "fused_bias_if_lif_stateful",
     "conv_neuron", "linear_neuron", "conv_bn_neuron", "fold_conv_bn",
 ]

@@ -24,6 +24,8 @@ F32, BF16, F16, U8, I32 = 0, 1, 2, 3, 4
 SPIKE_SAME, SPIKE_U8 = 0, 1
 # threshold modes
 THR_SCALAR, THR_PER_CHANNEL, THR_PER_NEURON = 0, 1, 2
+# binary GEMM algorithms
+BGEMM_AUTO, BGEMM_POPC, BGEMM_MFMA_I8 = 0, 1, 2
 
 _p = C.c_void_p
 _i32 = C.c_int32
@@ -43,6 +45,19 @@ PROTOTYPES: dict[str, list] = {
         _i32,                  # channel_last
         _f32, _f32, _f32,      # decay, in_scale, v_reset
         _i32, _p,              # soft_reset, stream
+    ],
+    "snnk_pack_bits": [
+        _p, _i32, _p,          # src, src_dtype, dst
+        _i64, _i64, _i64,      # batch, rows, K
+        _i64, _i64, _i64,      # stride_b, stride_r, stride_k
+        _p,                    # stream
+    ],
+    "snnk_binary_gemm": [
+        _p, _p, _p, _i32,      # A, B, C, c_dtype
+        _i64, _i64, _i64, _i64,  # batch, M, N, K
+        _i64, _i64, _i64,      # lda, ldb, ldc
+        _i64, _i64, _i64,      # stride_a, stride_b, stride_c
+        _i32, _i32, _p,        # signed_w, algo, stream
     ],
 }
 
