@@ -29,22 +29,28 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 constexpr int kTile = 128;     // per wave, square
 constexpr int kStageW = 4;     // packed words per stage
 
-__device__ __forceinline__ u32x4 load_words(const uint32_t* row, int64_t w0, int64_t KW,
-                                            uint32_t last_mask, bool valid, bool vec_ok) {
-  u32x4 v = {0u, 0u, 0u, 0u};
-  if (!valid) return v;
-  if (vec_ok && w0 + kStageW <= KW) {
-    v = *reinterpret_cast<const u32x4*>(row + w0);
+// Four packed words of a row starting at word w0, all inside the row.
+template <bool VEC>
+__device__ __forceinline__ u32x4 load_full(const uint32_t* row, int64_t w0) {
+  if constexpr (VEC) {
+    return *reinterpret_cast<const u32x4*>(row + w0);
   } else {
-#pragma unroll
-    for (int j = 0; j < kStageW; ++j)
-      if (w0 + j < KW) v[j] = row[w0 + j];
+    u32x4 v;
+    v[0] = row[w0]; v[1] = row[w0 + 1]; v[2] = row[w0 + 2]; v[3] = row[w0 + 3];
+    return v;
   }
-  if (w0 + kStageW >= KW) {  // the stage that holds the last word
-    const int64_t lw = KW - 1 - w0;
+}
+
+// The last (partial) stage: words past KW read as 0, the last word masked.
+__device__ __forceinline__ u32x4 load_tail(const uint32_t* row, int64_t w0, int64_t KW,
+                                           uint32_t last_mask) {
+  u32x4 v = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int j = 0; j < kStageW; ++j)
-      if (j == lw) v[j] &= last_mask;
+  for (int j = 0; j < kStageW; ++j) {
+    if (w0 + j < KW) {
+      uint32_t x = row[w0 + j];
+      v[j] = (w0 + j == KW - 1) ? (x & last_mask) : x;
+    }
   }
   return v;
 }
@@ -59,11 +65,34 @@ __device__ __forceinline__ i32x4 expand(uint32_t w, int g) {
   return r;
 }
 
-template <bool SIGNED, bool OUT_F32>
+// 4 MFMA k-steps of one stage for the wave's 4x4 accumulator tiles.
+template <bool SIGNED>
+__device__ __forceinline__ void mfma_stage(i32x16 (&acc)[4][4], const u32x4 (&a)[4],
+                                           const u32x4 (&b)[4], int g, int (&rowpop)[4]) {
+#pragma unroll
+  for (int kk = 0; kk < kStageW; ++kk) {
+    i32x4 fa[4], fb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      fa[t] = expand(a[t][kk], g);
+      fb[t] = expand(b[t][kk], g);
+      if constexpr (SIGNED) rowpop[t] += __builtin_popcount(a[t][kk]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+// n_main stages of 4 full words run without guards; a final partial stage
+// (KW % 4 != 0, or a masked last word) runs once with guards.
+template <bool SIGNED, bool OUT_F32, bool VEC>
 __global__ __launch_bounds__(64) void bgemm_mfma_kernel(
     const uint32_t* __restrict__ A, const uint32_t* __restrict__ B, void* __restrict__ Cv,
-    int64_t M, int64_t N, int64_t KW, uint32_t last_mask, int64_t lda, int64_t ldb,
-    int64_t ldc, int64_t sA, int64_t sB, int64_t sC, int vec_ok) {
+    int64_t M, int64_t N, int64_t KW, int64_t n_main, int has_tail, uint32_t last_mask,
+    int64_t lda, int64_t ldb, int64_t ldc, int64_t sA, int64_t sB, int64_t sC) {
   const int lane = threadIdx.x;
   const int r32 = lane & 31, g = lane >> 5;
   const int64_t bz = blockIdx.z;
@@ -72,16 +101,14 @@ __global__ __launch_bounds__(64) void bgemm_mfma_kernel(
   A += bz * sA;
   B += bz * sB;
 
+  // Rows past M / N read row 0: they only feed outputs that are never stored.
   const uint32_t* arow[4];
   const uint32_t* brow[4];
-  bool aval[4], bval[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int64_t m = m_base + t * 32 + r32, n = n_base + t * 32 + r32;
-    aval[t] = m < M;
-    bval[t] = n < N;
-    arow[t] = A + (aval[t] ? m : 0) * lda;
-    brow[t] = B + (bval[t] ? n : 0) * ldb;
+    arow[t] = A + (m < M ? m : 0) * lda;
+    brow[t] = B + (n < N ? n : 0) * ldb;
   }
 
   i32x16 acc[4][4];
@@ -93,35 +120,32 @@ __global__ __launch_bounds__(64) void bgemm_mfma_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
   int rowpop[4] = {0, 0, 0, 0};
 
+  // Stage s < n_main holds 4 full words; stage n_main (if has_tail) is the
+  // guarded partial stage.  The loads of stage s+1 are issued before stage s
+  // runs on the MFMA pipe; one MFMA block serves every stage.
+  const int64_t n_stages = n_main + has_tail;
   u32x4 a_cur[4], b_cur[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    a_cur[t] = load_words(arow[t], 0, KW, last_mask, aval[t], vec_ok);
-    b_cur[t] = load_words(brow[t], 0, KW, last_mask, bval[t], vec_ok);
-  }
-  for (int64_t w0 = 0; w0 < KW; w0 += kStageW) {
-    u32x4 a_nxt[4], b_nxt[4];
-    const int64_t wn = w0 + kStageW;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      a_nxt[t] = load_words(arow[t], wn, KW, last_mask, aval[t] && wn < KW, vec_ok);
-      b_nxt[t] = load_words(brow[t], wn, KW, last_mask, bval[t] && wn < KW, vec_ok);
-    }
-#pragma unroll
-    for (int kk = 0; kk < kStageW; ++kk) {
-      i32x4 fa[4], fb[4];
+  auto load_stage = [&](u32x4 (&a)[4], u32x4 (&b)[4], int64_t st) {
+    const int64_t w0 = st * kStageW;
+    if (st < n_main) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        fa[t] = expand(a_cur[t][kk], g);
-        fb[t] = expand(b_cur[t][kk], g);
-        if constexpr (SIGNED) rowpop[t] += __builtin_popcount(a_cur[t][kk]);
+        a[t] = load_full<VEC>(arow[t], w0);
+        b[t] = load_full<VEC>(brow[t], w0);
       }
+    } else if (st < n_stages) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      for (int t = 0; t < 4; ++t) {
+        a[t] = load_tail(arow[t], w0, KW, last_mask);
+        b[t] = load_tail(brow[t], w0, KW, last_mask);
+      }
     }
+  };
+  load_stage(a_cur, b_cur, 0);
+  for (int64_t s = 0; s < n_stages; ++s) {
+    u32x4 a_nxt[4], b_nxt[4];
+    load_stage(a_nxt, b_nxt, s + 1);
+    mfma_stage<SIGNED>(acc, a_cur, b_cur, g, rowpop);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       a_cur[t] = a_nxt[t];
@@ -163,13 +187,21 @@ int launch_mfma(const uint32_t* A, const uint32_t* B, void* C, int64_t batch, in
                 int64_t sB, int64_t sC, hipStream_t stream) {
   const int64_t KW = (K + 31) / 32;
   const uint32_t last_mask = (K % 32) ? ((1u << (K % 32)) - 1u) : 0xFFFFFFFFu;
+  const bool has_tail = (KW % kStageW != 0) || (last_mask != 0xFFFFFFFFu);
+  const int64_t n_main = has_tail ? KW / kStageW - ((KW % kStageW == 0) ? 1 : 0) : KW / kStageW;
   const int64_t gx = (N + kTile - 1) / kTile, gy = (M + kTile - 1) / kTile;
   if (gx > 0x7FFFFFFFll || gy > 65535 || batch > 65535) return SNNK_EUNSUPPORTED;
   // 16-byte row loads need 16-byte aligned rows
-  const int vec_ok = aligned(A, 16) && aligned(B, 16) && (lda % 4 == 0) && (ldb % 4 == 0) &&
-                     (batch == 1 || ((sA % 4 == 0) && (sB % 4 == 0)));
-  hipLaunchKernelGGL((bgemm_mfma_kernel<SIGNED, OUT_F32>), dim3(gx, gy, batch), dim3(64), 0,
-                     stream, A, B, C, M, N, KW, last_mask, lda, ldb, ldc, sA, sB, sC, vec_ok);
+  const bool vec = aligned(A, 16) && aligned(B, 16) && (lda % 4 == 0) && (ldb % 4 == 0) &&
+                   (batch == 1 || ((sA % 4 == 0) && (sB % 4 == 0)));
+  if (vec)
+    hipLaunchKernelGGL((bgemm_mfma_kernel<SIGNED, OUT_F32, true>), dim3(gx, gy, batch), dim3(64),
+                       0, stream, A, B, C, M, N, KW, n_main, has_tail ? 1 : 0, last_mask, lda,
+                       ldb, ldc, sA, sB, sC);
+  else
+    hipLaunchKernelGGL((bgemm_mfma_kernel<SIGNED, OUT_F32, false>), dim3(gx, gy, batch), dim3(64),
+                       0, stream, A, B, C, M, N, KW, n_main, has_tail ? 1 : 0, last_mask, lda,
+                       ldb, ldc, sA, sB, sC);
   return launch_status();
 }
 
