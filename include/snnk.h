@@ -133,6 +133,57 @@ int snnk_binary_gemm(const uint32_t* A, const uint32_t* B, void* C, int32_t c_dt
                      int64_t stride_a, int64_t stride_b, int64_t stride_c,
                      int32_t signed_w, int32_t algo, void* stream);
 
+/*
+ * Fused conv3x3 (stride 1, pad 1) + folded-BN bias + multi-step LIF
+ * (+ 2x2 max-pool, stride 2), bf16 MFMA with fp32 accumulation; only spikes
+ * are written.
+ *
+ * Replaces the layer pair
+ *   FusedConvBNNeuron._conv_bn / forward   snn_compiler/nn/modules.py:324-357
+ *     (F.conv2d + fused_bias_if_lif, snn_compiler/kernels/fused.py:101-114)
+ *   followed by nn.MaxPool2d(2, 2)         snn_compiler/zoo/vgg.py:56,101-105
+ *
+ * x        [T][B][H][W][Cin] bf16 (NHWC per step), Cin % 32 == 0
+ * w        [Cout][9*Cin] bf16, k = (kh*3 + kw)*Cin + cin, BN folded
+ *          (fold_conv_bn, snn_compiler/kernels/fused.py:585-599); Cout % 32 == 0
+ * bias     [Cout] fp32 or NULL
+ * spikes_out [T][B][Ho][Wo][Cout] bf16 0/1, Ho = H/2, Wo = W/2 when pool
+ * preact_out NULL, or [T][B][H][W][Cout] fp32 conv + bias instead of spikes
+ *          (no LIF, pool must be 0): for numerical checks
+ * LIF: v = decay*v + in_scale*(conv + bias); spike v >= v_threshold;
+ *      hard reset to v_reset or soft reset (v -= v_threshold); state starts at 0.
+ * tile_hint: -1 picks the tile shape from the problem size; 0..5 force one.
+ */
+int snnk_conv3x3_bn_lif(const uint16_t* x, const uint16_t* w, const float* bias,
+                        uint16_t* spikes_out, float* preact_out,
+                        int64_t T, int64_t B, int64_t H, int64_t W,
+                        int64_t Cin, int64_t Cout, int32_t pool,
+                        float decay, float in_scale, float v_threshold,
+                        float v_reset, int32_t soft_reset, int32_t tile_hint,
+                        void* stream);
+
+/*
+ * Input layer: a static image presented at all T steps.  conv3x3 (pad 1)
+ * in fp32 computed once per pixel, then T LIF steps on that constant input.
+ * Replaces the first FusedConvBNNeuron of VGGSNN (snn_compiler/zoo/vgg.py:57-68)
+ * fed with the image repeated over T.
+ *
+ * image [B][Cin][H][W] fp32 (NCHW); w [Cout][Cin][3][3] fp32 (BN folded);
+ * bias [Cout] fp32 or NULL; spikes_out [T][B][H][W][Cout] bf16 0/1.
+ */
+int snnk_conv3x3_image_lif(const float* image, const float* w, const float* bias,
+                           uint16_t* spikes_out, int64_t T, int64_t B, int64_t Cin,
+                           int64_t H, int64_t W, int64_t Cout, float decay,
+                           float in_scale, float v_threshold, float v_reset,
+                           int32_t soft_reset, void* stream);
+
+/*
+ * Layout change [N][C][HW] -> [N][HW][C] with conversion to bf16
+ * (src_dtype F32 / BF16 / F16 / U8; fp32 rounds to nearest even).
+ */
+int snnk_to_nhwc_bf16(const void* src, int32_t src_dtype, uint16_t* dst,
+                      int64_t N, int64_t C, int64_t HW, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -1,0 +1,153 @@
+// Input layer of a spiking CNN and layout conversion (gfx950).
+//
+// snnk_conv3x3_image_lif: a static image [B][Cin][H][W] (fp32, Cin small,
+// e.g. RGB) is presented at every one of T steps (the VGG16-SNN input
+// convention, examples/vgg16_snn/vgg16_test.py:243 and BASELINE's config).
+// The conv output is therefore the same at every step: it is computed once
+// per (pixel, channel) in fp32 on the VALU (K = 9*Cin is far too small for
+// MFMA) and the LIF recurrence runs T times on that constant current.
+// Output spikes go to NHWC bf16 [T][B][H][W][Cout] for the next MFMA layer.
+//
+// snnk_to_nhwc_bf16: [N][C][HW] (fp32/bf16/f16/u8) -> [N][HW][C] bf16.
+#include "snnk_common.h"
+
+namespace snnk {
+namespace {
+
+__global__ __launch_bounds__(256) void conv_image_lif_kernel(
+    const float* __restrict__ img, const float* __restrict__ w, const float* __restrict__ bias,
+    uint16_t* __restrict__ out, int T, int B, int Cin, int H, int W, int Cout, float decay,
+    float in_scale, float vth, float v_reset, int soft_reset) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(B) * H * W * Cout;
+  if (idx >= total) return;
+  const int n = static_cast<int>(idx % Cout);
+  const int64_t p = idx / Cout;  // (b, y, x)
+  const int x = static_cast<int>(p % W);
+  const int y = static_cast<int>((p / W) % H);
+  const int b = static_cast<int>(p / (static_cast<int64_t>(W) * H));
+  float acc = 0.0f;
+  for (int c = 0; c < Cin; ++c) {
+    const float* ip = img + (static_cast<int64_t>(b) * Cin + c) * H * W;
+    const float* wp = w + (static_cast<int64_t>(n) * Cin + c) * 9;
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+      const int ys = y + kh - 1;
+      if (ys < 0 || ys >= H) continue;
+#pragma unroll
+      for (int kw = 0; kw < 3; ++kw) {
+        const int xs = x + kw - 1;
+        if (xs < 0 || xs >= W) continue;
+        acc = __fadd_rn(acc, __fmul_rn(ip[ys * W + xs], wp[kh * 3 + kw]));
+      }
+    }
+  }
+  const float u = bias ? __fadd_rn(acc, bias[n]) : acc;
+  float v = 0.0f;
+  const int64_t step = static_cast<int64_t>(B) * H * W * Cout;
+  for (int t = 0; t < T; ++t) {
+    const float h = __fadd_rn(__fmul_rn(decay, v), __fmul_rn(in_scale, u));
+    const bool s = h >= vth;
+    v = s ? (soft_reset ? __fsub_rn(h, vth) : v_reset) : h;
+    out[t * step + idx] = s ? 0x3F80u : 0u;
+  }
+}
+
+template <typename Raw>
+__device__ __forceinline__ uint16_t to_bf16_bits(Raw v);
+template <> __device__ __forceinline__ uint16_t to_bf16_bits<float>(float v) {
+  // round to nearest even (inputs here are finite)
+  uint32_t u = __float_as_uint(v);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+template <> __device__ __forceinline__ uint16_t to_bf16_bits<uint8_t>(uint8_t v) {
+  return v ? 0x3F80u : 0u;
+}
+
+// 32x32 tile transpose through LDS: reads along HW, writes along C.
+template <typename Raw, int KIND>  // KIND: 0 generic (float/u8), 1 bf16 copy, 2 f16
+__global__ __launch_bounds__(256) void to_nhwc_kernel(const Raw* __restrict__ src,
+                                                      uint16_t* __restrict__ dst, int64_t C,
+                                                      int64_t HW) {
+  __shared__ uint16_t tile[32][33];
+  const int64_t n = blockIdx.z;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * 32;
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t c = c0 + i, p = p0 + tx;
+    uint16_t v = 0;
+    if (c < C && p < HW) {
+      const Raw r = src[(n * C + c) * HW + p];
+      if constexpr (KIND == 0) v = to_bf16_bits<Raw>(r);
+      else if constexpr (KIND == 1) v = r;
+      else v = to_bf16_bits<float>(static_cast<float>(__builtin_bit_cast(_Float16, r)));
+    }
+    tile[i][tx] = v;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t p = p0 + i, c = c0 + tx;
+    if (c < C && p < HW) dst[(n * HW + p) * C + c] = tile[tx][i];
+  }
+}
+
+}  // namespace
+}  // namespace snnk
+
+using namespace snnk;
+
+extern "C" int snnk_conv3x3_image_lif(const float* image, const float* w, const float* bias,
+                                      uint16_t* spikes_out, int64_t T, int64_t B, int64_t Cin,
+                                      int64_t H, int64_t W, int64_t Cout, float decay,
+                                      float in_scale, float v_threshold, float v_reset,
+                                      int32_t soft_reset, void* stream) {
+  if (T < 0 || B < 0 || Cin <= 0 || H < 0 || W < 0 || Cout <= 0) return SNNK_EINVAL;
+  if (T == 0 || B == 0 || H == 0 || W == 0) return SNNK_OK;
+  if (image == nullptr || w == nullptr || spikes_out == nullptr) return SNNK_EINVAL;
+  if (B * H * W * Cout * T > (1ll << 40) || H > 0x7FFFFFFF || W > 0x7FFFFFFF ||
+      Cin > 4096 || Cout > 0x7FFFFFFF)
+    return SNNK_EUNSUPPORTED;
+  const int64_t total = B * H * W * Cout;
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
+  hipLaunchKernelGGL(conv_image_lif_kernel, dim3(blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), image, w, bias, spikes_out,
+                     static_cast<int>(T), static_cast<int>(B), static_cast<int>(Cin),
+                     static_cast<int>(H), static_cast<int>(W), static_cast<int>(Cout), decay,
+                     in_scale, v_threshold, v_reset, soft_reset ? 1 : 0);
+  return launch_status();
+}
+
+extern "C" int snnk_to_nhwc_bf16(const void* src, int32_t src_dtype, uint16_t* dst, int64_t N,
+                                 int64_t C, int64_t HW, void* stream) {
+  if (N < 0 || C < 0 || HW < 0) return SNNK_EINVAL;
+  if (N == 0 || C == 0 || HW == 0) return SNNK_OK;
+  if (src == nullptr || dst == nullptr) return SNNK_EINVAL;
+  const int64_t gx = (HW + 31) / 32, gy = (C + 31) / 32;
+  if (gx > 0x7FFFFFFFll || gy > 65535 || N > 65535) return SNNK_EUNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid(gx, gy, N);
+  switch (src_dtype) {
+    case SNNK_F32:
+      hipLaunchKernelGGL((to_nhwc_kernel<float, 0>), grid, dim3(256), 0, s,
+                         static_cast<const float*>(src), dst, C, HW);
+      break;
+    case SNNK_U8:
+      hipLaunchKernelGGL((to_nhwc_kernel<uint8_t, 0>), grid, dim3(256), 0, s,
+                         static_cast<const uint8_t*>(src), dst, C, HW);
+      break;
+    case SNNK_BF16:
+      hipLaunchKernelGGL((to_nhwc_kernel<uint16_t, 1>), grid, dim3(256), 0, s,
+                         static_cast<const uint16_t*>(src), dst, C, HW);
+      break;
+    case SNNK_F16:
+      hipLaunchKernelGGL((to_nhwc_kernel<uint16_t, 2>), grid, dim3(256), 0, s,
+                         static_cast<const uint16_t*>(src), dst, C, HW);
+      break;
+    default:
+      return SNNK_EINVAL;
+  }
+  return launch_status();
+}

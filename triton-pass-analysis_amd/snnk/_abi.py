@@ -59,6 +59,27 @@ PROTOTYPES: dict[str, list] = {
         _i64, _i64, _i64,      # stride_a, stride_b, stride_c
         _i32, _i32, _p,        # signed_w, algo, stream
     ],
+    "snnk_conv3x3_bn_lif": [
+        _p, _p, _p,            # x, w, bias
+        _p, _p,                # spikes_out, preact_out
+        _i64, _i64, _i64, _i64,  # T, B, H, W
+        _i64, _i64, _i32,      # Cin, Cout, pool
+        _f32, _f32, _f32,      # decay, in_scale, v_threshold
+        _f32, _i32, _i32,      # v_reset, soft_reset, tile_hint
+        _p,                    # stream
+    ],
+    "snnk_conv3x3_image_lif": [
+        _p, _p, _p, _p,        # image, w, bias, spikes_out
+        _i64, _i64, _i64,      # T, B, Cin
+        _i64, _i64, _i64,      # H, W, Cout
+        _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
+        _i32, _p,              # soft_reset, stream
+    ],
+    "snnk_to_nhwc_bf16": [
+        _p, _i32, _p,          # src, src_dtype, dst
+        _i64, _i64, _i64,      # N, C, HW
+        _p,                    # stream
+    ],
 }
 
 _lib = None

@@ -1,0 +1,134 @@
+"""Fused conv3x3 + BN + LIF (+ 2x2 max-pool) on bf16 MFMA.
+
+The reference runs this block as three passes -- F.conv2d (cuDNN), the fused
+bias+LIF Triton kernel, then a separate nn.MaxPool2d
+(snn_compiler/nn/modules.py:324-357, snn_compiler/zoo/vgg.py:101-105).  Here
+it is one HIP kernel (csrc/conv.hip) that writes only spikes.
+
+Activations flow between layers as NHWC bf16 ``[T, B, H, W, C]`` tensors;
+``conv_bn_lif_pool`` accepts and returns the reference's ``[T, B, C, H, W]``
+labelling (the returned tensor is a channels-last view of the NHWC result).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _abi
+from .fused import fold_conv_bn
+from .neurons import neuron_params
+
+
+def prepare_conv3x3_weight(weight: torch.Tensor) -> torch.Tensor:
+    """[Cout, Cin, 3, 3] (BN already folded) -> bf16 [Cout, 9*Cin], k = (kh*3+kw)*Cin + cin."""
+    assert weight.ndim == 4 and weight.shape[2:] == (3, 3), tuple(weight.shape)
+    Cout, Cin = weight.shape[:2]
+    return weight.permute(0, 2, 3, 1).reshape(Cout, 9 * Cin).to(torch.bfloat16).contiguous()
+
+
+def to_nhwc_bf16(x_seq: torch.Tensor) -> torch.Tensor:
+    """[T, B, C, H, W] (any memory format, fp32/bf16/fp16/uint8) -> contiguous NHWC bf16
+    ``[T, B, H, W, C]``.  A bf16 channels-last input is returned as a view."""
+    assert x_seq.is_cuda and x_seq.ndim == 5, "expects a [T, B, C, H, W] GPU tensor"
+    T, B, C, H, W = x_seq.shape
+    nhwc = x_seq.permute(0, 1, 3, 4, 2)
+    if x_seq.dtype == torch.bfloat16 and nhwc.is_contiguous():
+        return nhwc
+    src = x_seq.contiguous()
+    out = torch.empty(T, B, H, W, C, device=x_seq.device, dtype=torch.bfloat16)
+    with torch.cuda.device(x_seq.device):
+        _abi.call("snnk_to_nhwc_bf16", src.data_ptr(), _abi.dtype_code(src.dtype),
+                  out.data_ptr(), T * B, C, H * W, _abi.stream(x_seq.device))
+    return out
+
+
+def conv3x3_bn_lif_nhwc(x: torch.Tensor, w_prep: torch.Tensor, bias: torch.Tensor | None, *,
+                        pool: bool, decay: float, in_scale: float, v_threshold: float,
+                        v_reset: float = 0.0, soft_reset: bool = False,
+                        out: torch.Tensor | None = None, tile_hint: int = -1) -> torch.Tensor:
+    """NHWC bf16 spikes in, NHWC bf16 spikes out ([T, B, Ho, Wo, Cout])."""
+    assert x.is_cuda and x.dtype == torch.bfloat16 and x.ndim == 5 and x.is_contiguous()
+    T, B, H, W, Cin = x.shape
+    Cout = w_prep.shape[0]
+    assert w_prep.dtype == torch.bfloat16 and w_prep.shape == (Cout, 9 * Cin) \
+        and w_prep.is_contiguous() and w_prep.device == x.device
+    if bias is not None:
+        assert bias.dtype == torch.float32 and bias.numel() == Cout and bias.is_contiguous()
+    Ho, Wo = (H // 2, W // 2) if pool else (H, W)
+    if out is None:
+        out = torch.empty(T, B, Ho, Wo, Cout, device=x.device, dtype=torch.bfloat16)
+    else:
+        assert out.shape == (T, B, Ho, Wo, Cout) and out.dtype == torch.bfloat16 \
+            and out.is_contiguous()
+    with torch.cuda.device(x.device):
+        _abi.call("snnk_conv3x3_bn_lif", x.data_ptr(), w_prep.data_ptr(), _abi.ptr(bias),
+                  out.data_ptr(), None, T, B, H, W, Cin, Cout, 1 if pool else 0,
+                  float(decay), float(in_scale), float(v_threshold), float(v_reset),
+                  1 if soft_reset else 0, int(tile_hint), _abi.stream(x.device))
+    return out
+
+
+def conv3x3_preact_nhwc(x: torch.Tensor, w_prep: torch.Tensor, bias: torch.Tensor | None,
+                        *, tile_hint: int = -1) -> torch.Tensor:
+    """fp32 conv + bias, NHWC ``[T, B, H, W, Cout]`` (the membrane input, no LIF)."""
+    assert x.is_cuda and x.dtype == torch.bfloat16 and x.ndim == 5 and x.is_contiguous()
+    T, B, H, W, Cin = x.shape
+    Cout = w_prep.shape[0]
+    assert w_prep.shape == (Cout, 9 * Cin) and w_prep.dtype == torch.bfloat16
+    pre = torch.empty(T, B, H, W, Cout, device=x.device, dtype=torch.float32)
+    with torch.cuda.device(x.device):
+        _abi.call("snnk_conv3x3_bn_lif", x.data_ptr(), w_prep.data_ptr(), _abi.ptr(bias),
+                  None, pre.data_ptr(), T, B, H, W, Cin, Cout, 0, 1.0, 1.0, 1.0, 0.0, 0,
+                  int(tile_hint), _abi.stream(x.device))
+    return pre
+
+
+def conv3x3_image_lif(image: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                      T: int, *, decay: float, in_scale: float, v_threshold: float,
+                      v_reset: float = 0.0, soft_reset: bool = False,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """Static image [B, Cin, H, W] fp32 shown at T steps -> NHWC bf16 spikes [T, B, H, W, Cout]."""
+    assert image.is_cuda and image.dtype == torch.float32 and image.ndim == 4
+    image = image.contiguous()
+    B, Cin, H, W = image.shape
+    Cout = weight.shape[0]
+    w = weight.float().contiguous()
+    assert w.shape == (Cout, Cin, 3, 3)
+    if bias is not None:
+        bias = bias.float().contiguous()
+    if out is None:
+        out = torch.empty(T, B, H, W, Cout, device=image.device, dtype=torch.bfloat16)
+    with torch.cuda.device(image.device):
+        _abi.call("snnk_conv3x3_image_lif", image.data_ptr(), w.data_ptr(), _abi.ptr(bias),
+                  out.data_ptr(), T, B, Cin, H, W, Cout, float(decay), float(in_scale),
+                  float(v_threshold), float(v_reset), 1 if soft_reset else 0,
+                  _abi.stream(image.device))
+    return out
+
+
+def conv_bn_lif_pool(x_seq, conv_w, conv_b, bn_w, bn_b, bn_mean, bn_var, bn_eps, *,
+                     pool: str | None = "max", neuron: str = "lif", tau: float = 2.0,
+                     decay: float | None = None, decay_input: bool = True,
+                     soft_reset: bool = False, v_threshold: float = 1.0,
+                     v_reset: float = 0.0, stride=1, padding=1, dilation=1, groups=1):
+    """conv3x3 + eval BN (folded) + IF/LIF + optional 2x2 max-pool, one kernel.
+
+    Signature of ``conv_bn_neuron`` (snn_compiler/kernels/fused.py:602-611)
+    plus ``pool``.  Only 3x3 / stride 1 / padding 1 / dilation 1 / groups 1,
+    Cin % 32 == 0, Cout % 32 == 0 and a float threshold are fused; for any
+    other conv use :func:`snnk.kernels.fused.conv_bn_neuron`.
+    Returns bf16 spikes labelled ``[T, B, Cout, Ho, Wo]`` in channels-last memory.
+    """
+    if (stride, padding, dilation, groups) not in ((1, 1, 1, 1), ((1, 1), (1, 1), (1, 1), 1)):
+        raise ValueError("conv_bn_lif_pool fuses 3x3 / stride 1 / padding 1 convs only")
+    if pool not in (None, "max"):
+        raise ValueError(f"unsupported pool {pool!r} (None or 'max')")
+    if isinstance(v_threshold, torch.Tensor):
+        raise ValueError("conv_bn_lif_pool takes a float threshold")
+    df, sc = neuron_params(neuron, tau, decay, decay_input)
+    new_w, new_b = fold_conv_bn(conv_w, conv_b, bn_w, bn_b, bn_mean, bn_var, bn_eps)
+    x = to_nhwc_bf16(x_seq)
+    out = conv3x3_bn_lif_nhwc(x, prepare_conv3x3_weight(new_w), new_b.float().contiguous(),
+                              pool=pool == "max", decay=df, in_scale=sc,
+                              v_threshold=float(v_threshold), v_reset=v_reset,
+                              soft_reset=soft_reset)
+    return out.permute(0, 1, 4, 2, 3)
