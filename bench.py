@@ -241,8 +241,85 @@ def bench_bgemm(args, dev):
     return rec
 
 
-WORKLOADS = {"lif": bench_lif, "bgemm": bench_bgemm}
-HEADLINE_ORDER = ["lif", "bgemm"]
+# --------------------------------------------------------------------------
+# Fused conv3x3 + BN + LIF + 2x2 max-pool
+# --------------------------------------------------------------------------
+BF16_PEAK_TFLOPS = 2516.6
+
+
+def _conv_block_params(g, Cin, Cout):
+    w = torch.randn(Cout, Cin, 3, 3, generator=g) * (2.0 / (Cin * 9)) ** 0.5  # Kaiming normal
+    gamma = torch.rand(Cout, generator=g) + 0.5
+    beta = torch.randn(Cout, generator=g) * 0.1
+    mean = torch.randn(Cout, generator=g) * 0.1
+    var = torch.rand(Cout, generator=g) + 0.5
+    return w, gamma, beta, mean, var
+
+
+def bench_conv(args, dev):
+    from snnk.kernels import conv as kc
+    from snnk.kernels.fused import fold_conv_bn
+    from oracle import fused as of
+
+    T, B, Cin, Cout, H, W = 4, 32, 128, 256, 16, 16
+    g = torch.Generator().manual_seed(0)
+    x = (torch.rand(T, B, Cin, H, W, generator=g) < 0.15).float()
+    w, gamma, beta, mean, var = _conv_block_params(g, Cin, Cout)
+    w2, b2 = fold_conv_bn(w, None, gamma, beta, mean, var, 1e-5)
+    wp = kc.prepare_conv3x3_weight(w2.to(dev))
+    bd = b2.to(dev).float().contiguous()
+    xd = kc.to_nhwc_bf16(x.to(dev))
+    flops = 2.0 * T * B * H * W * Cout * Cin * 9
+    set_bytes = xd.numel() * 2 + T * B * (H // 2) * (W // 2) * Cout * 2
+    nsets = max(2, math.ceil(ROTATE_BYTES / set_bytes))
+    xs = [xd.clone() for _ in range(nsets)]
+    outs = [torch.empty(T, B, H // 2, W // 2, Cout, device=dev, dtype=torch.bfloat16)
+            for _ in range(nsets)]
+
+    def step(i):
+        kc.conv3x3_bn_lif_nhwc(xs[i], wp, bd, pool=True, decay=0.5, in_scale=0.5,
+                               v_threshold=1.0, out=outs[i])
+
+    wall, kern_ms = time_gpu(step, nsets, args.steps, args.warmup)
+    ref, _ = of.conv_bn_lif_pool(x, w, None, gamma, beta, mean, var, 1e-5, pool=True)
+    agree = (outs[0].float().cpu().permute(0, 1, 4, 2, 3) == ref).float().mean().item()
+    # NCHW fp32 -> NHWC bf16 conversion at the block boundary (outside the step)
+    x_nchw = x.to(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        kc.to_nhwc_bf16(x_nchw)
+    e1.record()
+    torch.cuda.synchronize()
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    rec = {
+        "workload": "conv", "value": flops / wall / 1e12, "unit": "TFLOP/s",
+        "ms_per_step": wall * 1e3, "dtype": "bf16 x bf16 -> f32 acc, f32 LIF",
+        "config": {"workload": "conv3x3_bn_lif_maxpool_T4_B32_C128to256_16x16", "T": T, "B": B,
+                   "Cin": Cin, "Cout": Cout, "H": H, "W": W, "input_p": 0.15,
+                   "layout": "NHWC bf16 in/out", "rotating_sets": nsets},
+        "roofline": {"bound": "mfma", "kernel": "conv3x3_kernel",
+                     "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
+                     "algorithmic_flops": flops, "kernel_ms_mean": kern_ms},
+        "spike_agreement_vs_fp32": agree,
+        "nchw_to_nhwc_ms": e0.elapsed_time(e1) / 20,
+        "parity": agree >= 0.999,
+    }
+    if not args.no_cpu_baseline:
+        torch.set_num_threads(cpu_threads())
+        sec = time_cpu(lambda: of.conv_bn_lif_pool(x, w, None, gamma, beta, mean, var, 1e-5,
+                                                   pool=True), budget_s=6.0)
+        rec["cpu_baseline"] = {"value": flops / sec / 1e12, "unit": "TFLOP/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "oracle.fused.conv_bn_lif_pool (fold_conv_bn + "
+                                         "F.conv2d fp32 + LIF + max_pool2d) on the full config",
+                               "seconds_per_call": sec}
+    return rec
+
+
+WORKLOADS = {"lif": bench_lif, "bgemm": bench_bgemm, "conv": bench_conv}
+HEADLINE_ORDER = ["lif", "bgemm", "conv"]
 
 
 def main():

@@ -163,6 +163,26 @@ int snnk_conv3x3_bn_lif(const uint16_t* x, const uint16_t* w, const float* bias,
                         void* stream);
 
 /*
+ * Linear + bias + multi-step LIF on bf16 MFMA (fp32 accumulation), the same
+ * kernel as snnk_conv3x3_bn_lif run as a 1x1 conv over rows.
+ *
+ * Replaces FusedLinearNeuron.forward    snn_compiler/nn/modules.py:241-255
+ *   (F.linear + fused_bias_if_lif) and linear_neuron, snn_compiler/kernels/fused.py:554-579;
+ *   also the Conv1d-1x1 + BN + LIF projections of FusedSpikeAttention
+ *   (snn_compiler/nn/attention.py:117-131).
+ *
+ * x [T][R][K] bf16 (R rows per step, e.g. batch or batch*tokens; R % 4 == 0,
+ * K % 32 == 0), w [N][K] bf16 (nn.Linear layout, N % 32 == 0), bias [N] fp32
+ * or NULL; spikes_out [T][R][N] bf16 0/1, or preact_out [T][R][N] fp32
+ * (x.w^T + bias, no neuron).
+ */
+int snnk_linear_bias_lif(const uint16_t* x, const uint16_t* w, const float* bias,
+                         uint16_t* spikes_out, float* preact_out, int64_t T,
+                         int64_t R, int64_t K, int64_t N, float decay,
+                         float in_scale, float v_threshold, float v_reset,
+                         int32_t soft_reset, int32_t tile_hint, void* stream);
+
+/*
  * Input layer: a static image presented at all T steps.  conv3x3 (pad 1)
  * in fp32 computed once per pixel, then T LIF steps on that constant input.
  * Replaces the first FusedConvBNNeuron of VGGSNN (snn_compiler/zoo/vgg.py:57-68)

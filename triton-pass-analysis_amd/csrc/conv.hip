@@ -80,7 +80,14 @@ struct Cfg {
 
 __device__ __forceinline__ uint16_t spike_bf16(bool s) { return s ? 0x3F80u : 0u; }
 
-template <int WM, int WN, int TM, int TN, int KSPLIT, bool POOL, int MODE>
+// TAPS = 9: 3x3 conv, pad 1.  TAPS = 1: 1x1 conv, i.e. a Linear layer over
+// the rows of [T][rows][Cin] (H = 1, W = rows).
+template <int TAPS>
+__device__ __forceinline__ int tap_dy(int tap) { return TAPS == 9 ? tap / 3 - 1 : 0; }
+template <int TAPS>
+__device__ __forceinline__ int tap_dx(int tap) { return TAPS == 9 ? tap % 3 - 1 : 0; }
+
+template <int WM, int WN, int TM, int TN, int KSPLIT, bool POOL, int MODE, int TAPS>
 __global__ __launch_bounds__(64 * WM * WN * KSPLIT)
 void conv3x3_kernel(ConvArgs a) {
   using C = Cfg<WM, WN, TM, TN, KSPLIT, POOL, MODE>;
@@ -96,7 +103,7 @@ void conv3x3_kernel(ConvArgs a) {
   const int quad0 = blockIdx.x * C::kQuads;
   const int n0 = blockIdx.y * C::BN;
   const int HW = a.H * a.W;
-  const int K = 9 * a.Cin;
+  const int K = TAPS * a.Cin;
 
   // ---- per-thread A chunk geometry (fixed for the whole kernel) ----------
   // chunk c -> (group, row, 16-byte part); row -> (quad, pixel q, step t)
@@ -134,8 +141,8 @@ void conv3x3_kernel(ConvArgs a) {
     }
     uint32_t ok = row_ok ? (1u << 9) : 0u;
 #pragma unroll
-    for (int tap = 0; tap < 9; ++tap) {
-      const int ys = y + tap / 3 - 1, xs = xx + tap % 3 - 1;
+    for (int tap = 0; tap < TAPS; ++tap) {
+      const int ys = y + tap_dy<TAPS>(tap), xs = xx + tap_dx<TAPS>(tap);
       if (row_ok && ys >= 0 && ys < a.H && xs >= 0 && xs < a.W) ok |= 1u << tap;
     }
     a_off[i] = ((b * a.H + y) * a.W + xx) * a.Cin + part * 8;
@@ -196,12 +203,12 @@ void conv3x3_kernel(ConvArgs a) {
         // a group whose interleaved stage runs past K loads zeros
         const int sg = s * KSPLIT + a_kg[i];
         const int k0 = (sg < a.n_stages ? sg : 0) * kKS;
-        const int tap = static_cast<int>(fdiv(static_cast<uint32_t>(k0), a.div_cin));
+        const int tap = TAPS == 9 ? static_cast<int>(fdiv(static_cast<uint32_t>(k0), a.div_cin)) : 0;
         const int cin0 = k0 - tap * a.Cin;
         const int tg = tc * 4 + a_t[i];
         u32x4 z = {0u, 0u, 0u, 0u};
         if (((a_ok[i] >> tap) & 1u) && (a_ok[i] >> 9) && tg < a.T && sg < a.n_stages) {
-          const int dy = tap / 3 - 1, dx = tap % 3 - 1;
+          const int dy = tap_dy<TAPS>(tap), dx = tap_dx<TAPS>(tap);
           const int64_t off = static_cast<int64_t>(tg) * a.x_tstride + a_off[i] +
                               (dy * a.W + dx) * a.Cin + cin0;
           z = *reinterpret_cast<const u32x4*>(a.x + off);
@@ -334,19 +341,19 @@ void conv3x3_kernel(ConvArgs a) {
   }
 }
 
-template <int WM, int WN, int TM, int TN, int KSPLIT, bool POOL, int MODE>
+template <int WM, int WN, int TM, int TN, int KSPLIT, bool POOL, int MODE, int TAPS>
 int launch_cfg(const ConvArgs& a, hipStream_t stream) {
   using C = Cfg<WM, WN, TM, TN, KSPLIT, POOL, MODE>;
   const int gx = (a.n_quads + C::kQuads - 1) / C::kQuads;
   const int gy = (a.Cout + C::BN - 1) / C::BN;
-  hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, POOL, MODE>), dim3(gx, gy),
+  hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, POOL, MODE, TAPS>), dim3(gx, gy),
                      dim3(C::kThreads), 0, stream, a);
   return launch_status();
 }
 
 // Tile shape by problem size: enough blocks for 256 CUs, big tiles when M
 // allows, split-K when M*N is small.
-template <bool POOL, int MODE>
+template <bool POOL, int MODE, int TAPS>
 int dispatch(const ConvArgs& a, int tile_hint, hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(a.n_quads) * 16;  // per T-chunk
   int cfg = tile_hint;
@@ -358,12 +365,12 @@ int dispatch(const ConvArgs& a, int tile_hint, hipStream_t s) {
     else cfg = 4;                                              // 32 x 32, split-K 4
   }
   switch (cfg) {
-    case 0: return launch_cfg<2, 2, 2, 4, 1, POOL, MODE>(a, s);
-    case 1: return launch_cfg<4, 1, 2, 2, 1, POOL, MODE>(a, s);
-    case 2: return launch_cfg<2, 2, 2, 2, 1, POOL, MODE>(a, s);
-    case 3: return launch_cfg<2, 2, 1, 2, 1, POOL, MODE>(a, s);
-    case 4: return launch_cfg<1, 1, 1, 1, 4, POOL, MODE>(a, s);
-    case 5: return launch_cfg<1, 2, 1, 2, 2, POOL, MODE>(a, s);
+    case 0: return launch_cfg<2, 2, 2, 4, 1, POOL, MODE, TAPS>(a, s);
+    case 1: return launch_cfg<4, 1, 2, 2, 1, POOL, MODE, TAPS>(a, s);
+    case 2: return launch_cfg<2, 2, 2, 2, 1, POOL, MODE, TAPS>(a, s);
+    case 3: return launch_cfg<2, 2, 1, 2, 1, POOL, MODE, TAPS>(a, s);
+    case 4: return launch_cfg<1, 1, 1, 1, 4, POOL, MODE, TAPS>(a, s);
+    case 5: return launch_cfg<1, 2, 1, 2, 2, POOL, MODE, TAPS>(a, s);
     default: return SNNK_EINVAL;
   }
 }
@@ -411,7 +418,41 @@ extern "C" int snnk_conv3x3_bn_lif(const uint16_t* x, const uint16_t* w, const f
   a.decay = decay; a.in_scale = in_scale; a.vth = v_threshold; a.v_reset = v_reset;
   a.soft_reset = soft_reset ? 1 : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (preact) return dispatch<false, MODE_PREACT>(a, tile_hint, s);
-  if (pool) return dispatch<true, MODE_LIF>(a, tile_hint, s);
-  return dispatch<false, MODE_LIF>(a, tile_hint, s);
+  if (preact) return dispatch<false, MODE_PREACT, 9>(a, tile_hint, s);
+  if (pool) return dispatch<true, MODE_LIF, 9>(a, tile_hint, s);
+  return dispatch<false, MODE_LIF, 9>(a, tile_hint, s);
+}
+
+// Linear + bias + LIF over T: x [T][R][K] bf16 rows, w [N][K] bf16 (the
+// nn.Linear weight layout), one 1x1-conv pass of the same kernel.
+extern "C" int snnk_linear_bias_lif(const uint16_t* x, const uint16_t* w, const float* bias,
+                                    uint16_t* spikes_out, float* preact_out, int64_t T,
+                                    int64_t R, int64_t K, int64_t N, float decay,
+                                    float in_scale, float v_threshold, float v_reset,
+                                    int32_t soft_reset, int32_t tile_hint, void* stream) {
+  if (T < 0 || R < 0 || K <= 0 || N <= 0) return SNNK_EINVAL;
+  if (T == 0 || R == 0) return SNNK_OK;
+  if (x == nullptr || w == nullptr) return SNNK_EINVAL;
+  const bool preact = preact_out != nullptr;
+  if (!preact && spikes_out == nullptr) return SNNK_EINVAL;
+  if (K % kKS != 0 || N % 32 != 0 || R % 4 != 0) return SNNK_EUNSUPPORTED;
+  if (T * R * K > 0x7FFFFFFFll || R * K > 0x7FFFFFFFll || N * K > 0x7FFFFFFFll ||
+      T * R * N > (1ll << 40))
+    return SNNK_EUNSUPPORTED;
+  if (!aligned(x, 16) || !aligned(w, 16)) return SNNK_EALIGN;
+  ConvArgs a{};
+  a.x = x; a.w = w; a.bias = bias; a.out = spikes_out; a.pre = preact_out;
+  a.T = static_cast<int>(T); a.B = 1; a.H = 1; a.W = static_cast<int>(R);
+  a.Cin = static_cast<int>(K); a.Cout = static_cast<int>(N);
+  a.Ho = 1; a.Wo = a.W;
+  a.n_quads = static_cast<int>(R / 4);
+  a.n_stages = static_cast<int>(K / kKS);
+  a.div_cin = make_fastdiv(static_cast<uint32_t>(K));
+  a.x_tstride = R * K;
+  a.o_tstride = R * N;
+  a.decay = decay; a.in_scale = in_scale; a.vth = v_threshold; a.v_reset = v_reset;
+  a.soft_reset = soft_reset ? 1 : 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (preact) return dispatch<false, MODE_PREACT, 1>(a, tile_hint, s);
+  return dispatch<false, MODE_LIF, 1>(a, tile_hint, s);
 }

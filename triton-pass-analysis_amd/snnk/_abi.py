@@ -68,6 +68,13 @@ PROTOTYPES: dict[str, list] = {
         _f32, _i32, _i32,      # v_reset, soft_reset, tile_hint
         _p,                    # stream
     ],
+    "snnk_linear_bias_lif": [
+        _p, _p, _p,            # x, w, bias
+        _p, _p,                # spikes_out, preact_out
+        _i64, _i64, _i64, _i64,  # T, R, K, N
+        _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
+        _i32, _i32, _p,        # soft_reset, tile_hint, stream
+    ],
     "snnk_conv3x3_image_lif": [
         _p, _p, _p, _p,        # image, w, bias, spikes_out
         _i64, _i64, _i64,      # T, B, Cin

@@ -1,0 +1,68 @@
+"""Linear + bias + LIF over T on bf16 MFMA (csrc/conv.hip, 1x1 mode).
+
+The reference runs F.linear (cuBLAS) and then its fused bias+LIF kernel
+(snn_compiler/nn/modules.py:241-255, snn_compiler/kernels/fused.py:554-579).
+Here the GEMM epilogue runs the neuron: each accumulator lane holds the four
+time steps of one (row, feature), so only spikes leave the kernel.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _abi
+
+
+def linear_fusable(x_seq: torch.Tensor, weight: torch.Tensor, v_threshold) -> bool:
+    """Shapes and arguments the fused kernel covers."""
+    if isinstance(v_threshold, torch.Tensor) or not x_seq.is_cuda:
+        return False
+    T, B = x_seq.shape[0], x_seq.shape[1]
+    K = x_seq[0, 0].numel() if x_seq.ndim > 2 else 1
+    N, Kw = weight.shape
+    return K == Kw and K % 32 == 0 and N % 32 == 0 and B % 4 == 0 and T > 0
+
+
+def _check(x, w, bias):
+    assert x.is_cuda and x.dtype == torch.bfloat16 and x.ndim == 3 and x.is_contiguous(), \
+        "x must be a contiguous bf16 [T, R, K] GPU tensor"
+    assert w.dtype == torch.bfloat16 and w.ndim == 2 and w.is_contiguous() \
+        and w.shape[1] == x.shape[2] and w.device == x.device
+    if bias is not None:
+        assert bias.dtype == torch.float32 and bias.numel() == w.shape[0] and bias.is_contiguous()
+
+
+def linear_bias_lif(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
+                    decay: float, in_scale: float, v_threshold: float, v_reset: float = 0.0,
+                    soft_reset: bool = False, out: torch.Tensor | None = None,
+                    tile_hint: int = -1) -> torch.Tensor:
+    """x [T, R, K] bf16, w [N, K] bf16 -> spikes [T, R, N] bf16."""
+    _check(x, w, bias)
+    T, R, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty(T, R, N, device=x.device, dtype=torch.bfloat16)
+    else:
+        assert out.shape == (T, R, N) and out.dtype == torch.bfloat16 and out.is_contiguous()
+    with torch.cuda.device(x.device):
+        _abi.call("snnk_linear_bias_lif", x.data_ptr(), w.data_ptr(), _abi.ptr(bias),
+                  out.data_ptr(), None, T, R, K, N, float(decay), float(in_scale),
+                  float(v_threshold), float(v_reset), 1 if soft_reset else 0, int(tile_hint),
+                  _abi.stream(x.device))
+    return out
+
+
+def linear_preact(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
+                  out: torch.Tensor | None = None, tile_hint: int = -1) -> torch.Tensor:
+    """x [T, R, K] bf16, w [N, K] bf16 -> fp32 x.w^T + bias [T, R, N] (no neuron)."""
+    _check(x, w, bias)
+    T, R, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty(T, R, N, device=x.device, dtype=torch.float32)
+    else:
+        assert out.shape == (T, R, N) and out.dtype == torch.float32 and out.is_contiguous()
+    with torch.cuda.device(x.device):
+        _abi.call("snnk_linear_bias_lif", x.data_ptr(), w.data_ptr(), _abi.ptr(bias),
+                  None, out.data_ptr(), T, R, K, N, 1.0, 1.0, 1.0, 0.0, 0, int(tile_hint),
+                  _abi.stream(x.device))
+    return out

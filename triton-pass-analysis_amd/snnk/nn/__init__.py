@@ -1,0 +1,12 @@
+"""Module layer (mirror of snn_compiler/nn/__init__.py)."""
+from .modules import (
+    IFNode, LIFNode, StatefulLIFNode, RateCodedLIFNode, RateCodedIFNode,
+    FusedConvNeuron, FusedLinearNeuron, FusedConvBNNeuron, FusedConvBNAddNeuron,
+    FusedAddNeuron, FusedConvBNLIFPool,
+)
+
+__all__ = [
+    "IFNode", "LIFNode", "StatefulLIFNode", "RateCodedLIFNode", "RateCodedIFNode",
+    "FusedConvNeuron", "FusedLinearNeuron", "FusedConvBNNeuron", "FusedConvBNAddNeuron",
+    "FusedAddNeuron", "FusedConvBNLIFPool",
+]

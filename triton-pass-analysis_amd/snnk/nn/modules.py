@@ -1,0 +1,332 @@
+"""nn.Module layer (mirror of snn_compiler/nn/modules.py).
+
+Every module takes ``[T, B, ...]`` and returns spikes ``[T, B, ...]``; the
+neuron arithmetic runs in libsnnk (HIP).  Constructor arguments follow the
+reference classes one to one; ``FusedConvBNLIFPool`` is new: the whole
+conv3x3 + BN + LIF + 2x2 max-pool block in one MFMA kernel.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ..kernels.neurons import if_lif, neuron_params
+from ..kernels.fused import (
+    fused_bias_if_lif, fused_bias_if_lif_rate, fused_bias_if_lif_stateful, fold_conv_bn,
+)
+from ..kernels.conv import (
+    prepare_conv3x3_weight, to_nhwc_bf16, conv3x3_bn_lif_nhwc,
+)
+from ..kernels.linear import linear_bias_lif, linear_fusable
+
+
+def _thr(module, v_threshold):
+    if isinstance(v_threshold, torch.Tensor):
+        module.register_buffer("v_threshold", v_threshold.float().contiguous())
+    else:
+        module.v_threshold = float(v_threshold)
+
+
+class IFNode(nn.Module):
+    """Integrate-and-fire (snn_compiler/nn/modules.py:26-49)."""
+
+    def __init__(self, *, decay: float = 1.0, soft_reset: bool = False,
+                 v_threshold=1.0, v_reset: float = 0.0, layout: str = "NCHW"):
+        super().__init__()
+        self.decay, self.soft_reset, self.v_reset, self.layout = decay, soft_reset, v_reset, layout
+        _thr(self, v_threshold)
+
+    def forward(self, x_seq):
+        return if_lif(x_seq if self.layout == "NHWC" else x_seq.contiguous(), neuron="if",
+                      decay=self.decay, soft_reset=self.soft_reset,
+                      v_threshold=self.v_threshold, v_reset=self.v_reset, layout=self.layout)
+
+
+class LIFNode(nn.Module):
+    """Leaky integrate-and-fire (snn_compiler/nn/modules.py:52-85)."""
+
+    def __init__(self, *, tau: float = 2.0, decay: float | None = None,
+                 decay_input: bool = True, soft_reset: bool = False, v_threshold=1.0,
+                 v_reset: float = 0.0, layout: str = "NCHW"):
+        super().__init__()
+        self.tau, self.decay, self.decay_input = tau, decay, decay_input
+        self.soft_reset, self.v_reset, self.layout = soft_reset, v_reset, layout
+        _thr(self, v_threshold)
+
+    def forward(self, x_seq):
+        return if_lif(x_seq if self.layout == "NHWC" else x_seq.contiguous(), neuron="lif",
+                      tau=self.tau, decay=self.decay, decay_input=self.decay_input,
+                      soft_reset=self.soft_reset, v_threshold=self.v_threshold,
+                      v_reset=self.v_reset, layout=self.layout)
+
+
+class StatefulLIFNode(nn.Module):
+    """LIF with carried membrane for T-chunked execution
+    (snn_compiler/nn/modules.py:553-586)."""
+
+    def __init__(self, *, tau: float = 2.0, decay: float | None = None,
+                 decay_input: bool = True, soft_reset: bool = False,
+                 v_threshold: float = 1.0, v_reset: float = 0.0, layout: str = "NCHW"):
+        super().__init__()
+        self.tau, self.decay, self.decay_input = tau, decay, decay_input
+        self.soft_reset, self.v_threshold = soft_reset, float(v_threshold)
+        self.v_reset, self.layout = v_reset, layout
+
+    def forward(self, x_seq, v_init=None, return_v=False):
+        return fused_bias_if_lif_stateful(
+            x_seq if self.layout == "NHWC" else x_seq.contiguous(), None, v_init=v_init,
+            return_v=return_v, neuron="lif", tau=self.tau, decay=self.decay,
+            decay_input=self.decay_input, soft_reset=self.soft_reset,
+            v_threshold=self.v_threshold, v_reset=self.v_reset, layout=self.layout)
+
+
+class RateCodedLIFNode(nn.Module):
+    """Spike count over T, fp32 [B, ...] (snn_compiler/nn/modules.py:487-522)."""
+
+    def __init__(self, *, tau: float = 2.0, decay: float | None = None,
+                 decay_input: bool = True, soft_reset: bool = False, v_threshold=1.0,
+                 v_reset: float = 0.0, layout: str = "NCHW"):
+        super().__init__()
+        self.tau, self.decay, self.decay_input = tau, decay, decay_input
+        self.soft_reset, self.v_reset, self.layout = soft_reset, v_reset, layout
+        _thr(self, v_threshold)
+
+    def forward(self, x_seq):
+        return fused_bias_if_lif_rate(
+            x_seq if self.layout == "NHWC" else x_seq.contiguous(), None, neuron="lif",
+            tau=self.tau, decay=self.decay, decay_input=self.decay_input,
+            soft_reset=self.soft_reset, v_threshold=self.v_threshold, v_reset=self.v_reset,
+            layout=self.layout)
+
+
+class RateCodedIFNode(nn.Module):
+    """IF spike count over T (snn_compiler/nn/modules.py:525-547)."""
+
+    def __init__(self, *, decay: float = 1.0, soft_reset: bool = False, v_threshold=1.0,
+                 v_reset: float = 0.0, layout: str = "NCHW"):
+        super().__init__()
+        self.decay, self.soft_reset, self.v_reset, self.layout = decay, soft_reset, v_reset, layout
+        _thr(self, v_threshold)
+
+    def forward(self, x_seq):
+        return fused_bias_if_lif_rate(
+            x_seq if self.layout == "NHWC" else x_seq.contiguous(), None, neuron="if",
+            decay=self.decay, soft_reset=self.soft_reset, v_threshold=self.v_threshold,
+            v_reset=self.v_reset, layout=self.layout)
+
+
+class _NeuronArgs:
+    def _set_neuron(self, neuron, tau, decay, decay_input, soft_reset, v_threshold, v_reset,
+                    layout):
+        self.neuron, self.tau, self.decay, self.decay_input = neuron, tau, decay, decay_input
+        self.soft_reset, self.v_reset, self.layout = soft_reset, v_reset, layout
+        _thr(self, v_threshold)
+
+    def _lif(self, y_seq, bias, residual=None):
+        return fused_bias_if_lif(
+            y_seq, bias, residual=residual, neuron=self.neuron, tau=self.tau,
+            decay=self.decay, decay_input=self.decay_input, soft_reset=self.soft_reset,
+            v_threshold=self.v_threshold, v_reset=self.v_reset, layout=self.layout)
+
+
+def _conv_seq(x_seq, w, bias, conv, layout):
+    """Vendor conv over [T*B, ...] returning [T, B, ...] in the module's layout."""
+    T, B = x_seq.shape[0], x_seq.shape[1]
+    x4 = x_seq.reshape(T * B, *x_seq.shape[2:])
+    if layout == "NHWC":
+        x4 = x4.contiguous(memory_format=torch.channels_last)
+        w = w.to(memory_format=torch.channels_last)
+    else:
+        x4 = x4.contiguous()
+    y = F.conv2d(x4, w, bias=bias, stride=conv["stride"], padding=conv["padding"],
+                 dilation=conv["dilation"], groups=conv["groups"])
+    if layout == "NHWC":
+        y = y.contiguous(memory_format=torch.channels_last)
+    else:
+        y = y.contiguous()
+    return y.view(T, B, *y.shape[1:])
+
+
+class FusedConvNeuron(nn.Module, _NeuronArgs):
+    """Conv2d (vendor, no bias) + bias + IF/LIF in one HIP kernel
+    (snn_compiler/nn/modules.py:160-217)."""
+
+    def __init__(self, in_ch, out_ch, kernel_size, *, stride=1, padding=0, dilation=1,
+                 groups=1, bias: bool = True, neuron: str = "if", tau: float = 2.0,
+                 decay: float | None = None, decay_input: bool = True,
+                 soft_reset: bool = False, v_threshold=1.0, v_reset: float = 0.0,
+                 layout: str = "NCHW"):
+        super().__init__()
+        conv = nn.Conv2d(in_ch, out_ch, kernel_size, stride=stride, padding=padding,
+                         dilation=dilation, groups=groups, bias=bias)
+        self.weight = nn.Parameter(conv.weight.detach().clone())
+        self.bias = nn.Parameter(conv.bias.detach().clone()) if bias else None
+        self.conv = dict(stride=conv.stride, padding=conv.padding, dilation=conv.dilation,
+                         groups=conv.groups)
+        self._set_neuron(neuron, tau, decay, decay_input, soft_reset, v_threshold, v_reset,
+                         layout)
+
+    def forward(self, x_seq):
+        y = _conv_seq(x_seq, self.weight, None, self.conv, self.layout)
+        b = None if self.bias is None else self.bias.float().contiguous()
+        return self._lif(y, b)
+
+
+class FusedLinearNeuron(nn.Module, _NeuronArgs):
+    """Linear + bias + IF/LIF (snn_compiler/nn/modules.py:220-255).
+
+    A bf16 input runs the fused bf16-MFMA GEMM + LIF kernel (fp32
+    accumulation) when the shape allows it (in_features % 32 == 0,
+    out_features % 32 == 0, batch % 4 == 0, float threshold).  Otherwise --
+    and always for fp32 inputs, keeping the reference's precision -- the
+    vendor GEMM in the input's dtype runs first, then the HIP neuron kernel.
+    """
+
+    def __init__(self, in_features, out_features, *, bias: bool = True, neuron: str = "if",
+                 tau: float = 2.0, decay: float | None = None, decay_input: bool = True,
+                 soft_reset: bool = False, v_threshold=1.0, v_reset: float = 0.0):
+        super().__init__()
+        lin = nn.Linear(in_features, out_features, bias=bias)
+        self.weight = nn.Parameter(lin.weight.detach().clone())
+        self.bias = nn.Parameter(lin.bias.detach().clone()) if bias else None
+        self._set_neuron(neuron, tau, decay, decay_input, soft_reset, v_threshold, v_reset,
+                         "NCHW")
+        self._w_bf16 = None
+
+    def forward(self, x_seq):
+        T, B = x_seq.shape[0], x_seq.shape[1]
+        b = None if self.bias is None else self.bias.float().contiguous()
+        if x_seq.dtype == torch.bfloat16 and linear_fusable(x_seq, self.weight,
+                                                            self.v_threshold):
+            if self._w_bf16 is None or self._w_bf16.device != x_seq.device:
+                self._w_bf16 = self.weight.detach().to(torch.bfloat16).contiguous()
+            df, sc = neuron_params(self.neuron, self.tau, self.decay, self.decay_input)
+            s = linear_bias_lif(x_seq.reshape(T, B, -1).to(torch.bfloat16).contiguous(),
+                                self._w_bf16, b, decay=df, in_scale=sc,
+                                v_threshold=self.v_threshold, v_reset=self.v_reset,
+                                soft_reset=self.soft_reset)
+            return s.to(x_seq.dtype)
+        y = F.linear(x_seq.reshape(T * B, -1), self.weight.to(x_seq.dtype), bias=None)
+        return self._lif(y.view(T, B, -1), b)
+
+
+class FusedConvBNNeuron(nn.Module, _NeuronArgs):
+    """Conv2d + eval BN + IF/LIF (snn_compiler/nn/modules.py:258-357).
+
+    fold_bn=True folds BN into the conv once; fold_bn=False keeps conv and BN
+    as separate vendor ops (bit-exact with the unfused network) and fuses
+    only the neuron.
+    """
+
+    def __init__(self, conv: nn.Conv2d, bn: nn.BatchNorm2d, *, fold_bn: bool = True,
+                 neuron: str = "if", tau: float = 2.0, decay: float | None = None,
+                 decay_input: bool = True, soft_reset: bool = False, v_threshold=1.0,
+                 v_reset: float = 0.0, layout: str = "NCHW"):
+        super().__init__()
+        assert bn.running_mean is not None
+        self.fold_bn = fold_bn
+        if fold_bn:
+            w, b = fold_conv_bn(conv.weight.detach(),
+                                conv.bias.detach() if conv.bias is not None else None,
+                                bn.weight.detach(), bn.bias.detach(),
+                                bn.running_mean.detach(), bn.running_var.detach(), bn.eps)
+            self.weight = nn.Parameter(w)
+            self.bias = nn.Parameter(b)
+        else:
+            self.weight = nn.Parameter(conv.weight.detach().clone())
+            self.register_parameter("conv_bias", nn.Parameter(conv.bias.detach().clone())
+                                    if conv.bias is not None else None)
+            for nm, t in (("bn_weight", bn.weight), ("bn_bias", bn.bias),
+                          ("bn_mean", bn.running_mean), ("bn_var", bn.running_var)):
+                self.register_buffer(nm, t.detach().clone())
+            self.bn_eps = bn.eps
+            self.bias = None
+        self.conv = dict(stride=conv.stride, padding=conv.padding, dilation=conv.dilation,
+                         groups=conv.groups)
+        self._set_neuron(neuron, tau, decay, decay_input, soft_reset, v_threshold, v_reset,
+                         layout)
+
+    def _conv_bn(self, x_seq):
+        if self.fold_bn:
+            y = _conv_seq(x_seq, self.weight, None, self.conv, self.layout)
+            return y, self.bias.float().contiguous()
+        y = _conv_seq(x_seq, self.weight, self.conv_bias, self.conv, self.layout)
+        T, B = y.shape[:2]
+        y4 = F.batch_norm(y.reshape(T * B, *y.shape[2:]), self.bn_mean, self.bn_var,
+                          self.bn_weight, self.bn_bias, training=False, eps=self.bn_eps)
+        if self.layout == "NHWC":
+            y4 = y4.contiguous(memory_format=torch.channels_last)
+        return y4.view(T, B, *y4.shape[1:]), None
+
+    def forward(self, x_seq):
+        y, bias = self._conv_bn(x_seq)
+        return self._lif(y, bias)
+
+
+class FusedConvBNAddNeuron(FusedConvBNNeuron):
+    """Conv + BN + residual add + IF/LIF (snn_compiler/nn/modules.py:360-443)."""
+
+    def forward(self, x_seq, residual_seq):
+        y, bias = self._conv_bn(x_seq)
+        return self._lif(y, bias, residual=residual_seq)
+
+
+class FusedAddNeuron(nn.Module, _NeuronArgs):
+    """a + b then IF/LIF (snn_compiler/nn/modules.py:446-481)."""
+
+    def __init__(self, *, neuron: str = "if", tau: float = 2.0, decay: float | None = None,
+                 decay_input: bool = True, soft_reset: bool = False, v_threshold=1.0,
+                 v_reset: float = 0.0, layout: str = "NCHW"):
+        super().__init__()
+        self._set_neuron(neuron, tau, decay, decay_input, soft_reset, v_threshold, v_reset,
+                         layout)
+
+    def forward(self, a_seq, b_seq):
+        a = a_seq if self.layout == "NHWC" else a_seq.contiguous()
+        return self._lif(a, None, residual=b_seq)
+
+
+class FusedConvBNLIFPool(nn.Module):
+    """conv3x3 + eval BN (folded) + IF/LIF + optional 2x2 max-pool, one MFMA kernel.
+
+    Replaces the reference's (FusedConvBNNeuron, nn.MaxPool2d) pair
+    (snn_compiler/nn/modules.py:258-357 then snn_compiler/zoo/vgg.py:101-105).
+    forward takes the reference's [T, B, C, H, W] (any memory format) and
+    returns bf16 spikes [T, B, C, Ho, Wo] in channels-last memory;
+    ``forward_nhwc`` chains layers on contiguous NHWC bf16 [T, B, H, W, C].
+    """
+
+    def __init__(self, conv: nn.Conv2d, bn: nn.BatchNorm2d | None, *, pool: str | None = "max",
+                 neuron: str = "lif", tau: float = 2.0, decay: float | None = None,
+                 decay_input: bool = True, soft_reset: bool = False, v_threshold: float = 1.0,
+                 v_reset: float = 0.0):
+        super().__init__()
+        if tuple(conv.kernel_size) != (3, 3) or tuple(conv.stride) != (1, 1) or \
+                tuple(conv.padding) != (1, 1) or tuple(conv.dilation) != (1, 1) or conv.groups != 1:
+            raise ValueError("FusedConvBNLIFPool needs a 3x3 / stride 1 / padding 1 conv")
+        if pool not in (None, "max"):
+            raise ValueError(f"unsupported pool {pool!r}")
+        w = conv.weight.detach().float()
+        b = conv.bias.detach().float() if conv.bias is not None else None
+        if bn is not None:
+            w, b = fold_conv_bn(w, b, bn.weight.detach().float(), bn.bias.detach().float(),
+                                bn.running_mean.detach().float(),
+                                bn.running_var.detach().float(), bn.eps)
+        if b is None:
+            b = torch.zeros(w.shape[0], device=w.device)
+        self.register_buffer("weight", w.contiguous())
+        self.register_buffer("bias", b.float().contiguous())
+        self.register_buffer("w_prep", prepare_conv3x3_weight(w))
+        self.pool = pool
+        self.decay_factor, self.input_scale = neuron_params(neuron, tau, decay, decay_input)
+        self.soft_reset, self.v_threshold, self.v_reset = soft_reset, float(v_threshold), v_reset
+
+    def forward_nhwc(self, x_nhwc, out=None, tile_hint=-1):
+        return conv3x3_bn_lif_nhwc(x_nhwc, self.w_prep, self.bias, pool=self.pool == "max",
+                                   decay=self.decay_factor, in_scale=self.input_scale,
+                                   v_threshold=self.v_threshold, v_reset=self.v_reset,
+                                   soft_reset=self.soft_reset, out=out, tile_hint=tile_hint)
+
+    def forward(self, x_seq):
+        return self.forward_nhwc(to_nhwc_bf16(x_seq)).permute(0, 1, 4, 2, 3)

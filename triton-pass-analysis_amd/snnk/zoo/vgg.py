@@ -1,0 +1,294 @@
+"""VGG-style spiking CNNs (mirror of snn_compiler/zoo/vgg.py) and a fused engine.
+
+``VGGSNN`` keeps the reference's module structure (Conv2d -> BatchNorm2d ->
+neuron, pools, a 3-layer classifier; snn_compiler/zoo/vgg.py:43-116) with the
+neurons running in libsnnk, and sizes FC1 from ``input_size`` (the reference
+hard-codes 224x224, snn_compiler/zoo/vgg.py:74).
+
+``FusedVGGSNN`` takes a built VGGSNN (max-pool variant) and runs the whole
+forward as fused HIP kernels over NHWC bf16 spikes:
+  * input layer: fp32 conv of the static image once per pixel + LIF over T
+    (snnk_conv3x3_image_lif);
+  * every other conv: conv3x3 + folded BN + LIF (+ 2x2 max) in one bf16-MFMA
+    kernel (snnk_conv3x3_bn_lif);
+  * FC1, FC2: Linear + bias + LIF in one bf16-MFMA kernel; FC3: Linear + bias.
+It returns ``[T, B, num_classes]`` like the reference; the caller averages
+over T (examples/vgg16_snn/vgg16_test.py:243).  ``capture`` records the
+forward in a HIP graph for a fixed batch.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ..nn.modules import IFNode, LIFNode, FusedConvBNLIFPool
+from ..kernels.conv import conv3x3_image_lif
+from ..kernels.fused import fold_conv_bn
+from ..kernels.linear import linear_bias_lif, linear_preact
+from ..kernels.neurons import neuron_params
+
+VGG16_CFG = [64, 64, "P", 128, 128, "P", 256, 256, 256, "P",
+             512, 512, 512, "P", 512, 512, 512, "P"]
+VGG19_CFG = [64, 64, "P", 128, 128, "P", 256, 256, 256, 256, "P",
+             512, 512, 512, 512, "P", 512, 512, 512, 512, "P"]
+VGG11_CFG = [64, "P", 128, "P", 256, 256, "P", 512, 512, "P", 512, 512, "P"]
+VGG13_CFG = [64, 64, "P", 128, 128, "P", 256, 256, "P", 512, 512, "P", 512, 512, "P"]
+
+
+def _neuron_factory(neuron, *, tau, decay_input, soft_reset, v_threshold, v_reset, layout):
+    if neuron == "if":
+        return IFNode(soft_reset=soft_reset, v_threshold=v_threshold, v_reset=v_reset,
+                      layout=layout)
+    return LIFNode(tau=tau, decay_input=decay_input, soft_reset=soft_reset,
+                   v_threshold=v_threshold, v_reset=v_reset, layout=layout)
+
+
+class VGGSNN(nn.Module):
+    """forward(x_seq [T, B, 3, H, W]) -> [T, B, num_classes]
+    (snn_compiler/zoo/vgg.py:43-116; ``input_size`` sizes FC1)."""
+
+    def __init__(self, cfg, num_classes=1000, *, in_ch=3, fc_hidden=4096, with_bn=True,
+                 neuron="lif", tau=2.0, decay_input=True, soft_reset=False, v_threshold=1.0,
+                 v_reset=0.0, layout="NCHW", pool="avg", input_size=224):
+        super().__init__()
+        feats = []
+        ch = in_ch
+        pool_layer = nn.AvgPool2d if pool == "avg" else nn.MaxPool2d
+        nk = dict(tau=tau, decay_input=decay_input, soft_reset=soft_reset,
+                  v_threshold=v_threshold, v_reset=v_reset)
+        for v in cfg:
+            if v == "P":
+                feats.append(pool_layer(2, 2))
+            else:
+                feats.append(nn.Conv2d(ch, v, 3, padding=1, bias=True))
+                if with_bn:
+                    feats.append(nn.BatchNorm2d(v))
+                feats.append(_neuron_factory(neuron, layout=layout, **nk))
+                ch = v
+        self.features = nn.Sequential(*feats)
+        n_pool = sum(1 for x in cfg if x == "P")
+        self.fc_in_dim = ch * (input_size // 2 ** n_pool) ** 2
+        self.classifier = nn.Sequential(
+            nn.Linear(self.fc_in_dim, fc_hidden),
+            _neuron_factory(neuron, layout="NCHW", **nk),
+            nn.Linear(fc_hidden, fc_hidden),
+            _neuron_factory(neuron, layout="NCHW", **nk),
+            nn.Linear(fc_hidden, num_classes),
+        )
+        self.cfg = list(cfg)
+        self.layout = layout
+        self.pool = pool
+        self.neuron_kind = neuron
+        self.neuron_kwargs = nk
+
+    def forward(self, x_seq):
+        T, B = x_seq.shape[0], x_seq.shape[1]
+        x = x_seq
+        for layer in self.features:
+            if isinstance(layer, (IFNode, LIFNode)):
+                x = layer(x)
+            else:
+                T_, B_ = x.shape[0], x.shape[1]
+                y = layer(x.reshape(T_ * B_, *x.shape[2:]))
+                x = y.view(T_, B_, *y.shape[1:])
+        x = x.contiguous().reshape(T, B, -1)
+        for layer in self.classifier:
+            if isinstance(layer, (IFNode, LIFNode)):
+                x = layer(x)
+            else:
+                T_, B_ = x.shape[0], x.shape[1]
+                x = layer(x.reshape(T_ * B_, -1)).view(T_, B_, -1)
+        return x
+
+
+def _maybe_init_bn(model):
+    """Meaningful BN running stats for synthetic benchmarks
+    (snn_compiler/zoo/vgg.py:118-126)."""
+    for m in model.modules():
+        if isinstance(m, nn.BatchNorm2d):
+            m.running_mean.copy_(torch.randn_like(m.running_mean) * 0.1)
+            m.running_var.copy_(torch.rand_like(m.running_var) + 0.5)
+            m.weight.data.copy_(torch.rand_like(m.weight) + 0.5)
+            m.bias.data.copy_(torch.randn_like(m.bias) * 0.1)
+
+
+@torch.no_grad()
+def seeded_init_(model: VGGSNN, seed: int = 0, gain: float = 1.0) -> VGGSNN:
+    """Deterministic init from one CPU generator, drawn layer by layer: conv
+    weight Kaiming-normal (fan_in, gain sqrt 2) x gain, conv bias
+    U(+-1/sqrt(fan_in)); BN running mean N(0, 0.1^2), running var U(0.5, 1.5),
+    weight U(0.5, 1.5), bias N(0, 0.1^2) (the _maybe_init_bn distributions);
+    Linear weight Kaiming-normal x gain, bias U(+-1/sqrt(fan_in))."""
+    g = torch.Generator().manual_seed(seed)
+    mods = list(model.features) + list(model.classifier)
+    for i, m in enumerate(mods):
+        if isinstance(m, nn.Conv2d):
+            fan_in = m.in_channels * 9
+            m.weight.copy_(torch.randn(m.weight.shape, generator=g) * math.sqrt(2.0 / fan_in) * gain)
+            m.bias.copy_((torch.rand(m.bias.shape, generator=g) * 2 - 1) / math.sqrt(fan_in))
+            bn = mods[i + 1] if i + 1 < len(mods) and isinstance(mods[i + 1], nn.BatchNorm2d) else None
+            if bn is not None:
+                bn.running_mean.copy_(torch.randn(bn.num_features, generator=g) * 0.1)
+                bn.running_var.copy_(torch.rand(bn.num_features, generator=g) + 0.5)
+                bn.weight.copy_(torch.rand(bn.num_features, generator=g) + 0.5)
+                bn.bias.copy_(torch.randn(bn.num_features, generator=g) * 0.1)
+        elif isinstance(m, nn.Linear):
+            fan_in = m.in_features
+            m.weight.copy_(torch.randn(m.weight.shape, generator=g) * math.sqrt(2.0 / fan_in) * gain)
+            m.bias.copy_((torch.rand(m.bias.shape, generator=g) * 2 - 1) / math.sqrt(fan_in))
+    return model
+
+
+def vgg11_snn(**kw): return _build(VGG11_CFG, **kw)
+def vgg13_snn(**kw): return _build(VGG13_CFG, **kw)
+def vgg16_snn(**kw): return _build(VGG16_CFG, **kw)
+def vgg19_snn(**kw): return _build(VGG19_CFG, **kw)
+
+
+def _build(cfg, *, fused=False, init_bn=True, seed=None, gain=1.0, **kwargs):
+    """Reference _build (snn_compiler/zoo/vgg.py:134-143); ``seed`` selects the
+    deterministic seeded_init_, ``fused`` returns a FusedVGGSNN engine."""
+    m = VGGSNN(cfg, **kwargs)
+    if seed is not None:
+        seeded_init_(m, seed, gain)
+    elif init_bn:
+        _maybe_init_bn(m)
+    m.eval()
+    if fused:
+        return FusedVGGSNN(m)
+    return m
+
+
+class FusedVGGSNN(nn.Module):
+    """VGGSNN (max-pool) run as fused HIP kernels on NHWC bf16 spikes."""
+
+    def __init__(self, model: VGGSNN, *, T: int = 4):
+        super().__init__()
+        if model.pool != "max":
+            raise ValueError("FusedVGGSNN fuses the max-pool variant (pool='max')")
+        self.T = T
+        nk = model.neuron_kwargs
+        self.decay, self.in_scale = neuron_params(model.neuron_kind, nk["tau"], None,
+                                                  nk["decay_input"])
+        self.vth, self.v_reset, self.soft = nk["v_threshold"], nk["v_reset"], nk["soft_reset"]
+        if isinstance(self.vth, torch.Tensor):
+            raise ValueError("FusedVGGSNN takes a float threshold")
+        mods = list(model.features)
+        groups = []  # (conv, bn, pool_after)
+        i = 0
+        while i < len(mods):
+            m = mods[i]
+            if isinstance(m, nn.Conv2d):
+                bn = mods[i + 1] if isinstance(mods[i + 1], nn.BatchNorm2d) else None
+                j = i + (2 if bn is not None else 1)
+                assert isinstance(mods[j], (LIFNode, IFNode)), "conv must be followed by a neuron"
+                pool = j + 1 < len(mods) and isinstance(mods[j + 1], nn.MaxPool2d)
+                groups.append((m, bn, pool))
+                i = j + (2 if pool else 1)
+            else:
+                raise ValueError(f"unexpected feature layer {type(m).__name__}")
+        conv0, bn0, self.pool0 = groups[0]
+        w0, b0 = conv0.weight.detach().float(), conv0.bias.detach().float()
+        if bn0 is not None:
+            w0, b0 = fold_conv_bn(w0, b0, bn0.weight.detach().float(), bn0.bias.detach().float(),
+                                  bn0.running_mean.detach().float(),
+                                  bn0.running_var.detach().float(), bn0.eps)
+        self.register_buffer("w0", w0.contiguous())
+        self.register_buffer("b0", b0.contiguous())
+        neuron_kw = dict(neuron=model.neuron_kind, tau=nk["tau"], decay_input=nk["decay_input"],
+                         soft_reset=nk["soft_reset"], v_threshold=nk["v_threshold"],
+                         v_reset=nk["v_reset"])
+        self.convs = nn.ModuleList(
+            FusedConvBNLIFPool(c, bn, pool="max" if p else None, **neuron_kw)
+            for c, bn, p in groups[1:])
+        lins = [m for m in model.classifier if isinstance(m, nn.Linear)]
+        assert len(lins) == 3
+        C_last = groups[-1][0].out_channels
+        fc1 = lins[0].weight.detach().float()
+        hw = fc1.shape[1] // C_last
+        # reference flattens NCHW (c, h, w); the engine's features are NHWC (h, w, c)
+        fc1 = fc1.view(fc1.shape[0], C_last, hw).permute(0, 2, 1).reshape(fc1.shape[0], -1)
+        self.register_buffer("fc1_w", fc1.to(torch.bfloat16).contiguous())
+        self.register_buffer("fc1_b", lins[0].bias.detach().float().contiguous())
+        self.register_buffer("fc2_w", lins[1].weight.detach().to(torch.bfloat16).contiguous())
+        self.register_buffer("fc2_b", lins[1].bias.detach().float().contiguous())
+        n_cls = lins[2].out_features
+        n_pad = (n_cls + 31) // 32 * 32
+        w3 = torch.zeros(n_pad, lins[2].in_features)
+        w3[:n_cls] = lins[2].weight.detach().float().cpu()
+        b3 = torch.zeros(n_pad)
+        b3[:n_cls] = lins[2].bias.detach().float().cpu()
+        self.register_buffer("fc3_w", w3.to(torch.bfloat16).contiguous())
+        self.register_buffer("fc3_b", b3.contiguous())
+        self.num_classes = n_cls
+        self._graphs = {}
+
+    def _lif(self):
+        return dict(decay=self.decay, in_scale=self.in_scale, v_threshold=self.vth,
+                    v_reset=self.v_reset, soft_reset=self.soft)
+
+    def features_nhwc(self, image: torch.Tensor, rates: list | None = None) -> torch.Tensor:
+        """image [B, 3, H, W] fp32 -> NHWC bf16 spikes of the last conv block.
+        ``rates`` (optional list) receives every layer's mean firing rate."""
+        x = conv3x3_image_lif(image, self.w0, self.b0, self.T, **self._lif())
+        if rates is not None:
+            rates.append(x.float().mean())
+        if self.pool0:
+            T, B, H, W, C = x.shape
+            x = x.view(T, B, H // 2, 2, W // 2, 2, C).amax(dim=(3, 5)).contiguous()
+        for conv in self.convs:
+            x = conv.forward_nhwc(x)
+            if rates is not None:
+                rates.append(x.float().mean())
+        return x
+
+    def forward(self, image: torch.Tensor, rates: list | None = None) -> torch.Tensor:
+        """image [B, 3, H, W] (static, shown at all T steps) or [T, B, 3, H, W]
+        with identical steps -> logits [T, B, num_classes] fp32."""
+        if image.ndim == 5:
+            assert image.shape[0] == self.T, f"expected T={self.T} steps"
+            image = image[0]
+        image = image.float().contiguous()
+        T, B = self.T, image.shape[0]
+        x = self.features_nhwc(image, rates).reshape(T, B, -1)
+        R = (B + 3) // 4 * 4
+        if R != B:
+            x = F.pad(x, (0, 0, 0, R - B))
+        x = linear_bias_lif(x, self.fc1_w, self.fc1_b, **self._lif())
+        if rates is not None:
+            rates.append(x[:, :B].float().mean())
+        x = linear_bias_lif(x, self.fc2_w, self.fc2_b, **self._lif())
+        if rates is not None:
+            rates.append(x[:, :B].float().mean())
+        y = linear_preact(x, self.fc3_w, self.fc3_b)
+        return y[:, :B, :self.num_classes]
+
+    @torch.no_grad()
+    def capture(self, B: int, H: int = 32, W: int = 32, device=None):
+        """Record forward for batch B in a HIP graph; returns (graph, in, out)."""
+        device = device or self.w0.device
+        x_in = torch.zeros(B, 3, H, W, device=device)
+        stream = torch.cuda.Stream(device)
+        stream.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(stream):
+            self.forward(x_in)  # warm-up outside the capture
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                y = self.forward(x_in)
+        torch.cuda.current_stream(device).wait_stream(stream)
+        torch.cuda.synchronize(device)
+        self._graphs[(B, H, W)] = (graph, x_in, y)
+        return graph, x_in, y
+
+    @torch.no_grad()
+    def run_graph(self, image: torch.Tensor) -> torch.Tensor:
+        key = (image.shape[0], image.shape[2], image.shape[3])
+        if key not in self._graphs:
+            self.capture(*key, device=image.device)
+        graph, x_in, y = self._graphs[key]
+        x_in.copy_(image)
+        graph.replay()
+        return y
