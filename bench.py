@@ -3,9 +3,11 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
-Workloads: ``lif`` (config 0).  A step is one pass of
-the operator over one batch of synthetic, seeded input that is resident in HBM
-before timing starts.  Buffers rotate over several sets (> 512 MiB in total)
+Workloads: ``vgg16`` (config 4, the headline:
+VGG16-SNN T=4 B=32 images/s, with the B=1/56 curve and per-layer kernel
+rooflines), ``lif`` (config 0), ``bgemm`` (config 1), ``conv`` (config 2).
+A step is one pass of the hot path over one batch of synthetic, seeded input
+that is resident in HBM before timing starts.  Buffers rotate over several sets (> 512 MiB in total)
 so that the 256 MiB MALL cannot serve a step from the previous step's data.
 
 Timing: K steps are captured in a HIP graph and replayed; the replay is
@@ -318,8 +320,136 @@ def bench_conv(args, dev):
     return rec
 
 
-WORKLOADS = {"lif": bench_lif, "bgemm": bench_bgemm, "conv": bench_conv}
-HEADLINE_ORDER = ["lif", "bgemm", "conv"]
+# --------------------------------------------------------------------------
+# VGG16-SNN end to end (the headline)
+# --------------------------------------------------------------------------
+def _vgg_layer_steps(eng, image, T):
+    """(name, flops, step(out_idx)) for every kernel of one forward, each fed
+    the activations the engine itself produced."""
+    from snnk.kernels.conv import conv3x3_image_lif
+    from snnk.kernels.linear import linear_bias_lif, linear_preact
+
+    B = image.shape[0]
+    lif = eng._lif()
+    steps = []
+    x = conv3x3_image_lif(image, eng.w0, eng.b0, T, **lif)
+    H, W, C0 = x.shape[2], x.shape[3], x.shape[4]
+    o0 = torch.empty_like(x)
+    steps.append(("L1 image 3->%d %dx%d" % (C0, H, W), 2.0 * B * H * W * C0 * 27,
+                  lambda: conv3x3_image_lif(image, eng.w0, eng.b0, T, out=o0, **lif)))
+    for li, conv in enumerate(eng.convs):
+        xin = x
+        x = conv.forward_nhwc(xin)
+        _, _, H, W, Cin = xin.shape
+        Cout = x.shape[-1]
+        out = torch.empty_like(x)
+        flops = 2.0 * T * B * H * W * Cout * Cin * 9
+        name = "L%d conv %d->%d %dx%d%s" % (li + 2, Cin, Cout, H, W,
+                                           " +pool" if conv.pool else "")
+        steps.append((name, flops, (lambda c=conv, a=xin, o=out: c.forward_nhwc(a, out=o))))
+    R = (B + 3) // 4 * 4
+    f = x.reshape(T, B, -1)
+    if R != B:
+        f = torch.nn.functional.pad(f, (0, 0, 0, R - B))
+    f = f.contiguous()
+    for nm, w, b, last in (("FC1", eng.fc1_w, eng.fc1_b, False),
+                           ("FC2", eng.fc2_w, eng.fc2_b, False),
+                           ("FC3", eng.fc3_w, eng.fc3_b, True)):
+        fin = f
+        f = (linear_preact(fin, w, b) if last else linear_bias_lif(fin, w, b, **lif))
+        out = torch.empty_like(f)
+        flops = 2.0 * T * B * w.shape[0] * w.shape[1]
+        name = "%s %d->%d" % (nm, w.shape[1], w.shape[0])
+        if last:
+            steps.append((name, flops, (lambda a=fin, w=w, b=b, o=out: linear_preact(a, w, b, out=o))))
+        else:
+            steps.append((name, flops, (lambda a=fin, w=w, b=b, o=out:
+                                        linear_bias_lif(a, w, b, out=o, **lif))))
+    return steps
+
+
+def bench_vgg(args, dev):
+    from snnk.zoo import vgg16_snn
+    from oracle import vgg as ov
+
+    T = 4
+    eng = vgg16_snn(num_classes=10, pool="max", input_size=32, seed=0, fused=True).to(dev)
+    params = ov.make_params(0)
+    recs = {}
+    for B in (32, 1, 56):
+        g = torch.Generator().manual_seed(B)
+        img_cpu = torch.randn(B, 3, 32, 32, generator=g)
+        nsets = 4
+        imgs = [img_cpu.to(dev) for _ in range(nsets)]
+        graph, x_in, y_out = eng.capture(B, device=dev)
+
+        def step(i, graph=graph, x_in=x_in, imgs=imgs):
+            x_in.copy_(imgs[i])
+            graph.replay()
+
+        # whole forward: time graph replays (they cannot be nested in a capture)
+        for i in range(args.warmup):
+            step(i % nsets)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for i in range(args.steps):
+            step(i % nsets)
+        e1.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / args.steps
+        gpu_ms = e0.elapsed_time(e1) / args.steps
+        logits = eng.run_graph(imgs[0]).mean(0).cpu()
+        ref = ov.forward(params, img_cpu, T).mean(0)
+        ok = bool(torch.equal(logits.argmax(-1), ref.argmax(-1))) and \
+            ((logits - ref).abs().max() / ref.abs().max()).item() < 1e-3
+        recs[B] = dict(B=B, img_s=B / wall, ms=wall * 1e3, gpu_ms=gpu_ms, parity=ok,
+                       img_cpu=img_cpu)
+    # per-layer kernels at B=32, each replayed alone in a graph
+    B = 32
+    image = recs[32]["img_cpu"].to(dev)
+    layers = []
+    for name, flops, fn in _vgg_layer_steps(eng, image, T):
+        _, ms = time_gpu(lambda i, fn=fn: fn(), 1, args.steps, args.warmup)
+        ach = flops / (ms * 1e-3) / 1e12
+        layers.append({"layer": name, "gflop": flops / 1e9, "kernel_ms": ms,
+                       "tflops": ach, "frac_bf16_peak": ach / BF16_PEAK_TFLOPS})
+    dom = max(layers, key=lambda r: r["kernel_ms"])
+    flops_fwd = sum(r["gflop"] for r in layers) * 1e9
+    r32 = recs[32]
+    rec = {
+        "workload": "vgg16", "value": r32["img_s"], "unit": "images/s",
+        "ms_per_step": r32["ms"], "dtype": "bf16 MFMA (fp32 acc), fp32 LIF; fp32 input layer",
+        "config": {"workload": "vgg16_snn_32x32_T4_B32_fc512-4096-4096-10", "model": "VGG16-SNN",
+                   "T": T, "global_batch": 32, "input": "[B,3,32,32] N(0,1) repeated over T",
+                   "pool": "max", "neuron": "LIF tau=2 theta=1 hard reset 0",
+                   "init": "seeded Kaiming + BN stats (gain 1)"},
+        "roofline": {"bound": "mfma", "kernel": dom["layer"], "achieved": dom["tflops"],
+                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": dom["tflops"] / BF16_PEAK_TFLOPS, "traffic": None,
+                     "algorithmic_flops": dom["gflop"] * 1e9, "kernel_ms_mean": dom["kernel_ms"]},
+        "forward_gflop": flops_fwd / 1e9,
+        "forward_tflops": flops_fwd / (r32["gpu_ms"] * 1e-3) / 1e12,
+        "layers": layers,
+        "batch_curve": [{"B": r["B"], "images_per_s": r["img_s"], "ms_per_forward": r["ms"],
+                         "parity": r["parity"]} for r in recs.values()],
+        "parity": all(r["parity"] for r in recs.values()),
+    }
+    if not args.no_cpu_baseline:
+        torch.set_num_threads(cpu_threads())
+        img = recs[32]["img_cpu"]
+        sec = time_cpu(lambda: ov.forward(params, img, T), budget_s=8.0)
+        rec["cpu_baseline"] = {"value": 32 / sec, "unit": "images/s",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "oracle.vgg.forward (torch CPU fp32 restatement of "
+                                         "VGGSNN, max-pool) at B=32, T=4",
+                               "seconds_per_call": sec}
+    return rec
+
+
+WORKLOADS = {"vgg16": bench_vgg, "lif": bench_lif, "bgemm": bench_bgemm, "conv": bench_conv}
+HEADLINE_ORDER = ["vgg16", "lif", "bgemm", "conv"]
 
 
 def main():
@@ -354,11 +484,13 @@ def main():
         "dtype": head["dtype"],
         "data": "synthetic (seeded torch CPU generator), random-init weights",
         "config": {**head["config"], "parallelism": "none (1 GPU)"},
+        **({"layers": head["layers"], "batch_curve": head["batch_curve"],
+            "forward_tflops": head["forward_tflops"]} if "layers" in head else {}),
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
         "parity": head["parity"],
         "components": {n: {k: r[k] for k in ("value", "unit", "ms_per_step", "roofline",
-                                             "parity", "cpu_baseline") if k in r}
+                                             "parity", "cpu_baseline", "config") if k in r}
                        for n, r in recs.items() if n != names[0]},
     }
     print(json.dumps(out), flush=True)
