@@ -41,6 +41,7 @@ extern "C" {
 /* ---- spike output formats ------------------------------------------- */
 #define SNNK_SPIKE_SAME  0   /* 0/1 in the input's element type            */
 #define SNNK_SPIKE_U8    1   /* 0/1 as uint8                                */
+#define SNNK_SPIKE_BF16  2   /* 0/1 as bf16 (input for the MFMA layers)      */
 
 /* ---- threshold modes (snn_compiler/kernels/neurons.py:66-68) --------- */
 #define SNNK_THR_SCALAR      0
@@ -181,6 +182,35 @@ int snnk_linear_bias_lif(const uint16_t* x, const uint16_t* w, const float* bias
                          int64_t R, int64_t K, int64_t N, float decay,
                          float in_scale, float v_threshold, float v_reset,
                          int32_t soft_reset, int32_t tile_hint, void* stream);
+
+/*
+ * Spike self-attention core: per (batch, head) and step t, integer
+ * S = Q K^T and O = S V on int8 MFMA over {0,1} spikes (no softmax), then
+ * a multi-step LIF on in_scale * O (in_scale = scale / tau for a LIF with
+ * decay_input).  Counts are exact integers; with power-of-two scales the
+ * membrane arithmetic is exact in fp32.
+ *
+ * Replaces the attention part of FusedSpikeAttention.forward
+ *   snn_compiler/nn/attention.py:141-152: kv = K^T V (bmm or
+ *   spike_ktv_popcount, snn_compiler/kernels/attention.py:245-258), then
+ *   spike_av_lif (snn_compiler/kernels/attention.py:107-137); over integers
+ *   (Q K^T) V == Q (K^T V).
+ *
+ * q, k, v: bf16 spikes; element (t, token row r = b*N + n, head h, dim dd) at
+ *   ptr + t*step + r*row + h*d + dd (q/k/v may be column slices of one
+ *   [T][B*N][3*H*d] projection output).  N <= 64 tokens, d <= 64.
+ * spikes_out: bf16, element (t, r, h*d + dd) at out + t*out_step + r*out_row + h*d + dd.
+ * s_counts: NULL or int32 [T][B][H][N][N] (Q K^T); o_counts: NULL or int32
+ *   [T][B][H][N][d] ((Q K^T) V).
+ */
+int snnk_spike_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         int64_t q_row, int64_t k_row, int64_t v_row,
+                         int64_t q_step, int64_t k_step, int64_t v_step,
+                         uint16_t* spikes_out, int64_t out_row, int64_t out_step,
+                         int32_t* s_counts, int32_t* o_counts,
+                         int64_t T, int64_t B, int64_t H, int64_t N, int64_t d,
+                         float decay, float in_scale, float v_threshold,
+                         float v_reset, int32_t soft_reset, void* stream);
 
 /*
  * Input layer: a static image presented at all T steps.  conv3x3 (pad 1)

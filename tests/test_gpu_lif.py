@@ -195,3 +195,11 @@ def test_i64_offsets_large_T():
     u = tail_y.float() + bias.cpu()[ch].view(1, -1)
     ref, _, _ = on.lif_multistep(u, neuron="lif")
     assert torch.equal(tail_s.float(), ref)
+
+
+def test_bf16_spike_output_from_fp32():
+    x_cpu = _randn((4, 8, 32, 8, 8), seed=21, scale=1.5)
+    for src in (x_cpu, x_cpu.half()):
+        s = snnk.if_lif(src.to(DEV), neuron="lif", spike_dtype=torch.bfloat16)
+        assert s.dtype == torch.bfloat16
+        assert torch.equal(s.cpu().float(), on.naive_if_lif(src, neuron="lif").float())

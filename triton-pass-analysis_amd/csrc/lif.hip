@@ -130,12 +130,14 @@ __device__ __forceinline__ uint32_t channel_of(const LifArgs& a, uint64_t i) {
   return static_cast<uint32_t>(q % a.C64);
 }
 
-// Tag: input element type; SPK: 0 = spikes in the input type, 1 = uint8;
+// Tag: input element type; SPK: 0 = spikes in the input type, 1 = uint8,
+// 2 = bf16;
 // VEC: neurons per thread (VEC == 1 is the unaligned / ragged fallback).
 template <typename Tag, int SPK, int VEC, bool HAS_RES>
 __global__ __launch_bounds__(kBlock) void lif_kernel(LifArgs a) {
   typedef typename Tag::raw Raw;
-  typedef typename std::conditional<SPK == 0, Raw, uint8_t>::type SRaw;
+  typedef typename std::conditional<
+      SPK == 0, Raw, typename std::conditional<SPK == 1, uint8_t, uint16_t>::type>::type SRaw;
   const uint64_t i0 =
       (static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x) * VEC;
   if (i0 >= static_cast<uint64_t>(a.NCL)) return;  // NCL % VEC == 0 when VEC > 1
@@ -183,7 +185,8 @@ __global__ __launch_bounds__(kBlock) void lif_kernel(LifArgs a) {
           v[j] = s ? (a.soft_reset ? __fsub_rn(h, thr[j]) : a.v_reset) : h;
           cnt[j] += s ? 1.0f : 0.0f;
           if constexpr (SPK == 0) so.v[j] = spike_val<Tag>(s);
-          else so.v[j] = s ? 1 : 0;
+          else if constexpr (SPK == 1) so.v[j] = s ? 1 : 0;
+          else so.v[j] = s ? 0x3F80u : 0u;
         }
         if (s_out) {
           const uint64_t off = static_cast<uint64_t>(t0 + k) * ncl + i0;
@@ -214,7 +217,7 @@ int dispatch_vec(const LifArgs& a, bool has_res, hipStream_t stream) {
   constexpr int VEC = 16 / sizeof(typename Tag::raw);
   // The vector path needs every per-step row to start on a 16-byte boundary
   // of the input and spike buffers.
-  constexpr int SBYTES = SPK == 0 ? sizeof(typename Tag::raw) : 1;
+  constexpr int SBYTES = SPK == 0 ? sizeof(typename Tag::raw) : (SPK == 1 ? 1 : 2);
   bool vec_ok = (a.NCL % VEC == 0) && aligned(a.x, 16) &&
                 (!has_res || aligned(a.residual, 16)) &&
                 (a.spikes == nullptr || aligned(a.spikes, SBYTES * VEC)) &&
@@ -257,7 +260,8 @@ extern "C" int snnk_lif_forward(const void* x, int32_t x_dtype,
   if (spikes == nullptr && count_out == nullptr && v_out == nullptr) return SNNK_EINVAL;
   if (thr_mode < SNNK_THR_SCALAR || thr_mode > SNNK_THR_PER_NEURON) return SNNK_EINVAL;
   if (thr_mode != SNNK_THR_SCALAR && vth == nullptr) return SNNK_EINVAL;
-  if (spike_fmt != SNNK_SPIKE_SAME && spike_fmt != SNNK_SPIKE_U8) return SNNK_EINVAL;
+  if (spike_fmt != SNNK_SPIKE_SAME && spike_fmt != SNNK_SPIKE_U8 && spike_fmt != SNNK_SPIKE_BF16)
+    return SNNK_EINVAL;
   const bool need_c = bias != nullptr || thr_mode == SNNK_THR_PER_CHANNEL;
   if (need_c && (C <= 0 || HW <= 0)) return SNNK_EINVAL;
   if (C <= 0) C = 1;
@@ -283,13 +287,15 @@ extern "C" int snnk_lif_forward(const void* x, int32_t x_dtype,
   switch (x_dtype) {
     case SNNK_F32:
       return spike_fmt == SNNK_SPIKE_SAME ? dispatch_vec<F32, 0>(a, has_res, s)
-                                          : dispatch_vec<F32, 1>(a, has_res, s);
+             : spike_fmt == SNNK_SPIKE_U8 ? dispatch_vec<F32, 1>(a, has_res, s)
+                                          : dispatch_vec<F32, 2>(a, has_res, s);
     case SNNK_BF16:
-      return spike_fmt == SNNK_SPIKE_SAME ? dispatch_vec<BF16, 0>(a, has_res, s)
-                                          : dispatch_vec<BF16, 1>(a, has_res, s);
+      return spike_fmt == SNNK_SPIKE_U8 ? dispatch_vec<BF16, 1>(a, has_res, s)
+                                        : dispatch_vec<BF16, 0>(a, has_res, s);
     case SNNK_F16:
       return spike_fmt == SNNK_SPIKE_SAME ? dispatch_vec<F16, 0>(a, has_res, s)
-                                          : dispatch_vec<F16, 1>(a, has_res, s);
+             : spike_fmt == SNNK_SPIKE_U8 ? dispatch_vec<F16, 1>(a, has_res, s)
+                                          : dispatch_vec<F16, 2>(a, has_res, s);
     default:
       return SNNK_EINVAL;
   }

@@ -21,7 +21,7 @@ OK, EINVAL, EUNSUPPORTED, EALIGN = 0, -1, -2, -3
 # element types
 F32, BF16, F16, U8, I32 = 0, 1, 2, 3, 4
 # spike formats
-SPIKE_SAME, SPIKE_U8 = 0, 1
+SPIKE_SAME, SPIKE_U8, SPIKE_BF16 = 0, 1, 2
 # threshold modes
 THR_SCALAR, THR_PER_CHANNEL, THR_PER_NEURON = 0, 1, 2
 # binary GEMM algorithms
@@ -74,6 +74,16 @@ PROTOTYPES: dict[str, list] = {
         _i64, _i64, _i64, _i64,  # T, R, K, N
         _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
         _i32, _i32, _p,        # soft_reset, tile_hint, stream
+    ],
+    "snnk_spike_attention": [
+        _p, _p, _p,            # q, k, v
+        _i64, _i64, _i64,      # q_row, k_row, v_row
+        _i64, _i64, _i64,      # q_step, k_step, v_step
+        _p, _i64, _i64,        # spikes_out, out_row, out_step
+        _p, _p,                # s_counts, o_counts
+        _i64, _i64, _i64, _i64, _i64,  # T, B, H, N, d
+        _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
+        _i32, _p,              # soft_reset, stream
     ],
     "snnk_conv3x3_image_lif": [
         _p, _p, _p, _p,        # image, w, bias, spikes_out

@@ -1,14 +1,23 @@
 """Spike attention operators (mirror of snn_compiler/kernels/attention.py).
 
-``spike_ktv_popcount``: bit-exact K^T V of binary spikes through bit packing
-along the token axis and a popcount GEMM (reference
-snn_compiler/kernels/attention.py:245-258).
+* ``spike_ktv_popcount``: bit-exact K^T V through bit packing along the
+  token axis and a popcount GEMM (reference attention.py:245-258).
+* ``spike_av_lif``: the reference's fused ``(q @ kv) * scale -> LIF``
+  (attention.py:107-137): integer q @ kv on the GPU, then the HIP LIF kernel.
+* ``spike_attention``: the attention core on int8 MFMA straight from Q, K, V
+  spikes -- integer Q K^T and (Q K^T) V, then the LIF -- with the counts
+  optionally returned (csrc/attention.hip).
+* ``spike_self_attention``: the whole SSA block on tokens [T, B, N, D]:
+  fused QKV Linear + BN + LIF, the attention core, and the output Linear + BN.
 """
 from __future__ import annotations
 
 import torch
 
+from .. import _abi
 from .binary import pack_bits, _gemm_packed
+from .linear import linear_bias_lif, linear_preact
+from .neurons import if_lif, launch_lif, THR_SCALAR
 
 # popcount is native on gfx950 (v_bcnt_u32_b32); kept for API parity with
 # snn_compiler/kernels/attention.py:26-36.
@@ -35,3 +44,91 @@ def spike_ktv_popcount(k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
     vp = _pack_N(v.reshape(TBH, N, D))
     out = _gemm_packed(kp, vp, N, signed=False, algo="popc", out_dtype=torch.float32)
     return out.reshape(T, B, H, D, D)
+
+
+def _lif_scale(tau, decay, decay_input, scale):
+    dec = (1.0 if tau is None else 1.0 - 1.0 / tau) if decay is None else float(decay)
+    base = (1.0 / tau) if (decay_input and tau is not None) else 1.0
+    return dec, base * float(scale)
+
+
+def spike_av_lif(q, kv, *, scale, tau=2.0, decay=None, decay_input=True, v_threshold=0.5,
+                 v_reset=0.0, soft_reset=False):
+    """``(q @ kv) * scale -> LIF`` with q [T,B,heads,N,d] spikes and kv
+    [T,B,heads,d,d] integer counts; returns spikes like q.
+
+    Reference: snn_compiler/kernels/attention.py:107-137 (the scale is folded
+    into the LIF input scale, as there).  q @ kv is an exact integer product
+    (fp32 GEMM of small integers), the neuron runs in the HIP LIF kernel.
+    """
+    assert q.is_cuda and kv.is_cuda
+    T, B, H, N, D = q.shape
+    a = torch.matmul(q.float().contiguous(), kv.float().contiguous()).reshape(T, -1)
+    dec, in_scale = _lif_scale(tau, decay, decay_input, scale)
+    s = torch.empty_like(a)
+    launch_lif(a, thr=(THR_SCALAR, None, float(v_threshold)), spikes=s, decay=dec,
+               in_scale=in_scale, v_reset=v_reset, soft_reset=soft_reset)
+    return s.reshape(T, B, H, N, D).to(q.dtype)
+
+
+def spike_attention(q, k, v, *, B: int, N: int, heads: int, scale: float, tau: float = 2.0,
+                    decay: float | None = None, decay_input: bool = True,
+                    v_threshold: float = 0.5, v_reset: float = 0.0, soft_reset: bool = False,
+                    out: torch.Tensor | None = None, return_counts: bool = False):
+    """Attention core on int8 MFMA.
+
+    q, k, v: bf16 spikes ``[T, B*N, heads*d]`` (any row stride, e.g. column
+    slices of one QKV projection output).  Returns spikes ``[T, B*N, heads*d]``
+    bf16, and with ``return_counts`` also int32 ``S = Q K^T`` [T,B,heads,N,N]
+    and ``O = (Q K^T) V`` [T,B,heads,N,d].
+    """
+    for t in (q, k, v):
+        assert t.is_cuda and t.dtype == torch.bfloat16 and t.ndim == 3 and t.stride(2) == 1
+    T, R, HD = q.shape
+    assert R == B * N and HD % heads == 0 and k.shape == q.shape and v.shape == q.shape
+    d = HD // heads
+    dec, in_scale = _lif_scale(tau, decay, decay_input, scale)
+    if out is None:
+        out = torch.empty(T, R, HD, device=q.device, dtype=torch.bfloat16)
+    S = O = None
+    if return_counts:
+        S = torch.empty(T, B, heads, N, N, device=q.device, dtype=torch.int32)
+        O = torch.empty(T, B, heads, N, d, device=q.device, dtype=torch.int32)
+    with torch.cuda.device(q.device):
+        _abi.call("snnk_spike_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                  q.stride(1), k.stride(1), v.stride(1), q.stride(0), k.stride(0), v.stride(0),
+                  out.data_ptr(), out.stride(1), out.stride(0), _abi.ptr(S), _abi.ptr(O),
+                  T, B, heads, N, d, float(dec), float(in_scale), float(v_threshold),
+                  float(v_reset), 1 if soft_reset else 0, _abi.stream(q.device))
+    return (out, S, O) if return_counts else out
+
+
+def spike_self_attention(tokens, w_qkv, b_qkv, w_proj, b_proj, *, heads: int,
+                         scale: float = 0.125, tau: float = 2.0, vth_qkv: float = 1.0,
+                         vth_attn: float = 0.5, input_vth: float | None = None,
+                         return_intermediates: bool = False):
+    """Spikformer-style SSA block on tokens ``[T, B, N, D]``.
+
+    w_qkv: bf16 [3D, D] (q, k, v Linear weights stacked, BN folded), b_qkv fp32
+    [3D]; w_proj bf16 [D, D], b_proj fp32 [D].  Q, K, V = LIF(x W^T + b)
+    (threshold vth_qkv), attention spikes = LIF(scale * (Q K^T) V) per head
+    (threshold vth_attn), output = attn W_proj^T + b_proj (fp32).
+    ``input_vth`` applies the reference block's input LIF first
+    (snn_compiler/nn/attention.py:138).
+    """
+    T, B, N, D = tokens.shape
+    x = tokens.reshape(T, B * N, D)
+    if input_vth is not None:
+        x = if_lif(x.contiguous(), neuron="lif", tau=tau, v_threshold=input_vth,
+                   spike_dtype=torch.bfloat16)
+    x = x.to(torch.bfloat16).contiguous()
+    dec = 1.0 - 1.0 / tau
+    qkv = linear_bias_lif(x, w_qkv, b_qkv, decay=dec, in_scale=1.0 / tau, v_threshold=vth_qkv)
+    q, k, v = qkv[..., :D], qkv[..., D:2 * D], qkv[..., 2 * D:]
+    res = spike_attention(q, k, v, B=B, N=N, heads=heads, scale=scale, tau=tau,
+                          v_threshold=vth_attn, return_counts=return_intermediates)
+    attn = res[0] if return_intermediates else res
+    out = linear_preact(attn, w_proj, b_proj).view(T, B, N, D)
+    if return_intermediates:
+        return out, dict(qkv=qkv, attn=attn, S=res[1], O=res[2])
+    return out

@@ -101,8 +101,8 @@ def launch_lif(x, *, bias=None, residual=None, thr=(THR_SCALAR, None, 1.0),
     thr_mode, thr_t, thr_s = thr
     sfmt = _abi.SPIKE_SAME
     if spikes is not None and spikes.dtype != x.dtype:
-        assert spikes.dtype == torch.uint8, spikes.dtype
-        sfmt = _abi.SPIKE_U8
+        assert spikes.dtype in (torch.uint8, torch.bfloat16), spikes.dtype
+        sfmt = _abi.SPIKE_U8 if spikes.dtype == torch.uint8 else _abi.SPIKE_BF16
     with torch.cuda.device(x.device):
         _abi.call(
             "snnk_lif_forward",
@@ -134,7 +134,8 @@ def if_lif(
     Reference: snn_compiler/kernels/neurons.py:311-376 (``if_lif``).
     ``x_seq`` is ``[T, B, ...]`` fp32/bf16/fp16.  ``v_threshold`` is a float,
     a ``[C]`` or an ``[NCL]`` fp32 tensor.  ``spike_dtype`` (extension; default
-    the input dtype, as in the reference) may be ``torch.uint8``.
+    the input dtype, as in the reference) may be ``torch.uint8`` or
+    ``torch.bfloat16``.
     """
     check_flat(x_seq, layout)
     assert x_seq.dtype in (torch.float32, torch.float16, torch.bfloat16)
