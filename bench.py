@@ -5,7 +5,8 @@
 
 Workloads: ``vgg16`` (config 4, the headline:
 VGG16-SNN T=4 B=32 images/s, with the B=1/56 curve and per-layer kernel
-rooflines), ``lif`` (config 0), ``bgemm`` (config 1), ``conv`` (config 2).
+rooflines), ``lif`` (config 0), ``bgemm`` (config 1), ``conv`` (config 2),
+``ssa`` (config 3).
 A step is one pass of the hot path over one batch of synthetic, seeded input
 that is resident in HBM before timing starts.  Buffers rotate over several sets (> 512 MiB in total)
 so that the 256 MiB MALL cannot serve a step from the previous step's data.
@@ -448,8 +449,89 @@ def bench_vgg(args, dev):
     return rec
 
 
-WORKLOADS = {"vgg16": bench_vgg, "lif": bench_lif, "bgemm": bench_bgemm, "conv": bench_conv}
-HEADLINE_ORDER = ["vgg16", "lif", "bgemm", "conv"]
+# --------------------------------------------------------------------------
+# Spike self-attention block
+# --------------------------------------------------------------------------
+def bench_ssa(args, dev):
+    from snnk.kernels.attention import spike_attention
+    from snnk.kernels.linear import linear_bias_lif, linear_preact
+    from oracle import attention as oa
+
+    T, B, N, D, H = 4, 32, 64, 384, 8
+    g = torch.Generator().manual_seed(0)
+    x = (torch.rand(T, B, N, D, generator=g) < 0.2).float()
+    p = {f"w{n}": torch.randn(D, D, generator=g) * (2.0 / D) ** 0.5 for n in "qkvp"}
+    p.update({f"b{n}": torch.randn(D, generator=g) * 0.1 for n in "qkvp"})
+    w_qkv = torch.cat([p["wq"], p["wk"], p["wv"]]).to(dev, torch.bfloat16).contiguous()
+    b_qkv = torch.cat([p["bq"], p["bk"], p["bv"]]).to(dev).contiguous()
+    w_p, b_p = p["wp"].to(dev, torch.bfloat16).contiguous(), p["bp"].to(dev).contiguous()
+    nsets = 8
+    xs = [x.to(dev, torch.bfloat16).reshape(T, B * N, D).contiguous() for _ in range(nsets)]
+    qkvs = [torch.empty(T, B * N, 3 * D, device=dev, dtype=torch.bfloat16) for _ in range(nsets)]
+    attns = [torch.empty(T, B * N, D, device=dev, dtype=torch.bfloat16) for _ in range(nsets)]
+    outs = [torch.empty(T, B * N, D, device=dev) for _ in range(nsets)]
+    lif = dict(decay=0.5, in_scale=0.5, v_threshold=1.0)
+
+    def proj_qkv(i):
+        linear_bias_lif(xs[i], w_qkv, b_qkv, out=qkvs[i], **lif)
+
+    def attention(i):
+        q = qkvs[i]
+        spike_attention(q[..., :D], q[..., D:2 * D], q[..., 2 * D:], B=B, N=N, heads=H,
+                        scale=0.125, v_threshold=0.5, out=attns[i])
+
+    def proj_out(i):
+        linear_preact(attns[i], w_p, b_p, out=outs[i])
+
+    def step(i):
+        proj_qkv(i)
+        attention(i)
+        proj_out(i)
+
+    wall, _ = time_gpu(step, nsets, args.steps, args.warmup)
+    _, ms_qkv = time_gpu(proj_qkv, nsets, args.steps, args.warmup)
+    _, ms_att = time_gpu(attention, nsets, args.steps, args.warmup)
+    _, ms_out = time_gpu(proj_out, nsets, args.steps, args.warmup)
+    fl_qkv = 2.0 * T * B * N * D * 3 * D
+    fl_out = 2.0 * T * B * N * D * D
+    ops_att = 2.0 * 2 * T * B * H * N * N * (D // H)
+    ref = oa.ssa_forward(x, p, heads=H, scale=0.125, vth_qkv=1.0, vth_attn=0.5)
+    qkv_agree = (qkvs[0].cpu().float().view(T, B, N, 3 * D)
+                 == torch.cat([ref["q"], ref["k"], ref["v"]], -1)).float().mean().item()
+    kern = [("qkv_projection_lif", ms_qkv, fl_qkv, BF16_PEAK_TFLOPS, "TFLOP/s"),
+            ("attention_core_lif", ms_att, ops_att, INT8_PEAK_TOPS, "TOPS"),
+            ("output_projection", ms_out, fl_out, BF16_PEAK_TFLOPS, "TFLOP/s")]
+    per = [{"kernel": k, "kernel_ms": ms, "achieved": w / (ms * 1e-3) / 1e12, "peak": pk,
+            "unit": u, "frac": w / (ms * 1e-3) / 1e12 / pk} for k, ms, w, pk, u in kern]
+    dom = max(per, key=lambda r: r["kernel_ms"])
+    rec = {
+        "workload": "ssa", "value": (B * N) / wall, "unit": "tokens/s (T=4 block)",
+        "ms_per_step": wall * 1e3, "dtype": "bf16 projections (fp32 acc), int8 attention, fp32 LIF",
+        "config": {"workload": "spike_self_attention_T4_B32_N64_D384_H8", "T": T, "B": B,
+                   "N": N, "D": D, "heads": H, "scale": 0.125, "vth_qkv": 1.0, "vth_attn": 0.5},
+        "roofline": {"bound": "mfma", "kernel": dom["kernel"], "achieved": dom["achieved"],
+                     "peak": dom["peak"], "unit": dom["unit"], "frac": dom["frac"],
+                     "traffic": None, "kernel_ms_mean": dom["kernel_ms"]},
+        "kernels": per,
+        "block_gops": (fl_qkv + fl_out + ops_att) / 1e9,
+        "qkv_spike_agreement_vs_fp32": qkv_agree,
+        "parity": qkv_agree >= 0.999,
+    }
+    if not args.no_cpu_baseline:
+        torch.set_num_threads(cpu_threads())
+        sec = time_cpu(lambda: oa.ssa_forward(x, p, heads=H, scale=0.125, vth_qkv=1.0,
+                                              vth_attn=0.5), budget_s=6.0)
+        rec["cpu_baseline"] = {"value": (B * N) / sec, "unit": "tokens/s (T=4 block)",
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "oracle.attention.ssa_forward (torch CPU fp32 "
+                                         "projections + int64 attention) on the full config",
+                               "seconds_per_call": sec}
+    return rec
+
+
+WORKLOADS = {"vgg16": bench_vgg, "lif": bench_lif, "bgemm": bench_bgemm, "conv": bench_conv,
+             "ssa": bench_ssa}
+HEADLINE_ORDER = ["vgg16", "lif", "bgemm", "conv", "ssa"]
 
 
 def main():

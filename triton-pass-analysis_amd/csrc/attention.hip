@@ -8,12 +8,12 @@
 // (Q K^T) V == Q (K^T V), so the counts are identical; this kernel uses the
 // (Q K^T) V order and can return both count tensors for bit-exact checks.
 //
-// One block (one wave) per (batch, head).  Per step t the wave stages Q_t,
+// One block per (batch, head).  Per step t the block stages Q_t,
 // K_t and V_t^T of its head in LDS as int8 (zero padded to 64 tokens x 64
-// dims), computes S = Q K^T into accumulators, writes S to LDS as int8
+// dims; d % 8 == 0, rows 16-byte aligned), computes S = Q K^T into accumulators, writes S to LDS as int8
 // (0 <= S <= d <= 64), computes O = S V, and runs the LIF
 // v = decay*v + in_scale*O on O in registers; the membrane of every
-// (token, dim) stays in the same lane for all T steps.
+// (token, dim) stays in the same lane of the same wave for all T steps.
 #include "snnk_common.h"
 
 namespace snnk {
@@ -41,102 +41,130 @@ struct AttnArgs {
   int soft_reset;
 };
 
-__device__ __forceinline__ int8_t bit_of(uint16_t x) { return (x & 0x7FFFu) ? 1 : 0; }
+// Two words of bf16 pairs (4 elements) -> 4 bytes, 1 where the element is nonzero.
+__device__ __forceinline__ uint32_t bytes4(uint32_t lo, uint32_t hi) {
+  const uint32_t b0 = (lo & 0x7FFFu) ? 1u : 0u, b1 = (lo & 0x7FFF0000u) ? 1u : 0u;
+  const uint32_t b2 = (hi & 0x7FFFu) ? 1u : 0u, b3 = (hi & 0x7FFF0000u) ? 1u : 0u;
+  return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+}
 
+// Block = 4 waves for one (batch, head).  Staging is shared by the 256
+// threads; wave w computes S tile (w / NT, w % NT) when w < NT*NT and owns
+// O tile (w / DT, w % DT) -- with its LIF membrane -- when w < NT*DT.
 template <int NT, int DT>  // token tiles, dim tiles (32 each)
-__global__ __launch_bounds__(64) void ssa_attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void ssa_attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t qs[kMaxTok * kPitch];
   __shared__ __attribute__((aligned(16))) int8_t ks[kMaxTok * kPitch];
   __shared__ __attribute__((aligned(16))) int8_t vt[kMaxDim * kPitch];  // [dim][token]
   __shared__ __attribute__((aligned(16))) int8_t ss[kMaxTok * kPitch];  // S as int8
 
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int bh = blockIdx.x;
   const int b = bh / a.H, h = bh - b * a.H;
   const int r32 = lane & 31, g = lane >> 5;
+  // this block's (batch, head) slice: token row 0, column h*d
+  const int64_t row0 = static_cast<int64_t>(b) * a.N;
+  const uint16_t* qb = a.q + row0 * a.q_row + h * a.d;
+  const uint16_t* kb = a.k + row0 * a.k_row + h * a.d;
+  const uint16_t* vb = a.v + row0 * a.v_row + h * a.d;
 
-  float vm[NT][DT][16];
+  const bool has_s = wave < NT * NT;
+  const int si = wave / NT, sj = wave % NT;
+  const bool has_o = wave < NT * DT;
+  const int oi = wave / DT, od = wave % DT;
+  const int dd = od * 32 + r32;
+  uint16_t* ob = a.out + row0 * a.o_row + h * a.d + dd;
+  float vm[16];
 #pragma unroll
-  for (int i = 0; i < NT; ++i)
-#pragma unroll
-    for (int j = 0; j < DT; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) vm[i][j][e] = 0.0f;
+  for (int e = 0; e < 16; ++e) vm[e] = 0.0f;
 
   for (int t = 0; t < a.T; ++t) {
     // ---- stage Q_t, K_t (row = token) and V_t^T (row = dim) as int8 -------
-    {
-      const int n = lane;  // one token per lane
-      const bool ok = n < a.N;
-      const int64_t rq = static_cast<int64_t>(t) * a.q_t + (static_cast<int64_t>(b) * a.N + n) * a.q_row + h * a.d;
-      const int64_t rk = static_cast<int64_t>(t) * a.k_t + (static_cast<int64_t>(b) * a.N + n) * a.k_row + h * a.d;
-      const int64_t rv = static_cast<int64_t>(t) * a.v_t + (static_cast<int64_t>(b) * a.N + n) * a.v_row + h * a.d;
-      for (int dd = 0; dd < kMaxDim; ++dd) {
-        const bool in = ok && dd < a.d;
-        qs[n * kPitch + dd] = in ? bit_of(a.q[rq + dd]) : 0;
-        ks[n * kPitch + dd] = in ? bit_of(a.k[rk + dd]) : 0;
-        vt[dd * kPitch + n] = in ? bit_of(a.v[rv + dd]) : 0;
+    // 64 tokens x 8 chunks of 8 dims per tensor; consecutive threads walk
+    // along a token row with 16-byte loads; padding rows / dims are zeros.
+    const uint16_t* qt = qb + t * a.q_t;
+    const uint16_t* kt = kb + t * a.k_t;
+    const uint16_t* vtp = vb + t * a.v_t;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int ci = tid + 256 * m;
+      const int n = ci >> 3, c = ci & 7;
+      const bool in = n < a.N && c * 8 < a.d;
+      u32x4 wq = {0u, 0u, 0u, 0u}, wk = wq, wv = wq;
+      if (in) {
+        wq = *reinterpret_cast<const u32x4*>(qt + n * a.q_row + c * 8);
+        wk = *reinterpret_cast<const u32x4*>(kt + n * a.k_row + c * 8);
+        wv = *reinterpret_cast<const u32x4*>(vtp + n * a.v_row + c * 8);
+      }
+      u32x2 bq, bk;
+      bq[0] = bytes4(wq[0], wq[1]); bq[1] = bytes4(wq[2], wq[3]);
+      bk[0] = bytes4(wk[0], wk[1]); bk[1] = bytes4(wk[2], wk[3]);
+      *reinterpret_cast<u32x2*>(qs + n * kPitch + c * 8) = bq;
+      *reinterpret_cast<u32x2*>(ks + n * kPitch + c * 8) = bk;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w = wv[e >> 1] >> (16 * (e & 1));
+        vt[(c * 8 + e) * kPitch + n] = (w & 0x7FFFu) ? 1 : 0;
       }
     }
     __syncthreads();
 
-    // ---- S = Q K^T ---------------------------------------------------------
+    // ---- S = Q K^T (one 32x32 tile per wave) --------------------------------
+    if (has_s) {
+      i32x16 acc;
 #pragma unroll
-    for (int ti = 0; ti < NT; ++ti) {
+      for (int e = 0; e < 16; ++e) acc[e] = 0;
 #pragma unroll
-      for (int tj = 0; tj < NT; ++tj) {
-        i32x16 acc;
+      for (int kk = 0; kk < kMaxDim / 32; ++kk) {
+        const i32x4 fa = *reinterpret_cast<const i32x4*>(qs + (si * 32 + r32) * kPitch + kk * 32 + g * 16);
+        const i32x4 fb = *reinterpret_cast<const i32x4*>(ks + (sj * 32 + r32) * kPitch + kk * 32 + g * 16);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, acc, 0, 0, 0);
+      }
+      // register e of lane l: row 8*(e/4) + 4*g + e%4, column l%32
+      const int j = sj * 32 + r32;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] = 0;
-#pragma unroll
-        for (int kk = 0; kk < kMaxDim / 32; ++kk) {
-          const i32x4 fa = *reinterpret_cast<const i32x4*>(qs + (ti * 32 + r32) * kPitch + kk * 32 + g * 16);
-          const i32x4 fb = *reinterpret_cast<const i32x4*>(ks + (tj * 32 + r32) * kPitch + kk * 32 + g * 16);
-          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, acc, 0, 0, 0);
-        }
-        // register e of lane l: row 8*(e/4) + 4*g + e%4, column l%32
+      for (int e = 0; e < 16; ++e) {
+        const int i = si * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+        ss[i * kPitch + j] = static_cast<int8_t>(acc[e]);
+      }
+      if (a.s_counts) {
+        int32_t* sc = a.s_counts + ((static_cast<int64_t>(t) * a.B * a.H + bh) * a.N) * a.N;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int i = ti * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-          const int j = tj * 32 + r32;
-          ss[i * kPitch + j] = static_cast<int8_t>(acc[e]);
-          if (a.s_counts && i < a.N && j < a.N)
-            a.s_counts[((static_cast<int64_t>(t) * a.B * a.H + bh) * a.N + i) * a.N + j] = acc[e];
+          const int i = si * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+          if (i < a.N && j < a.N) sc[i * a.N + j] = acc[e];
         }
       }
     }
-    // tokens past N: S rows/cols are zero already (zero-padded Q, K); the
-    // columns j >= 32*NT are never read.
     __syncthreads();
 
-    // ---- O = S V and the LIF ---------------------------------------------------
+    // ---- O = S V and the LIF (one 32x32 tile per wave) --------------------------
+    if (has_o) {
+      i32x16 acc;
 #pragma unroll
-    for (int ti = 0; ti < NT; ++ti) {
+      for (int e = 0; e < 16; ++e) acc[e] = 0;
 #pragma unroll
-      for (int td = 0; td < DT; ++td) {
-        i32x16 acc;
+      for (int kk = 0; kk < NT; ++kk) {
+        const i32x4 fa = *reinterpret_cast<const i32x4*>(ss + (oi * 32 + r32) * kPitch + kk * 32 + g * 16);
+        const i32x4 fb = *reinterpret_cast<const i32x4*>(vt + (od * 32 + r32) * kPitch + kk * 32 + g * 16);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, acc, 0, 0, 0);
+      }
+      uint16_t* ot = ob + t * a.o_t;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] = 0;
-#pragma unroll
-        for (int kk = 0; kk < NT; ++kk) {
-          const i32x4 fa = *reinterpret_cast<const i32x4*>(ss + (ti * 32 + r32) * kPitch + kk * 32 + g * 16);
-          const i32x4 fb = *reinterpret_cast<const i32x4*>(vt + (td * 32 + r32) * kPitch + kk * 32 + g * 16);
-          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, acc, 0, 0, 0);
-        }
-        const int dd = td * 32 + r32;
+      for (int e = 0; e < 16; ++e) {
+        const int i = oi * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+        const float hm = __fadd_rn(__fmul_rn(a.decay, vm[e]), __fmul_rn(a.in_scale, static_cast<float>(acc[e])));
+        const bool sp = hm >= a.vth;
+        vm[e] = sp ? (a.soft_reset ? __fsub_rn(hm, a.vth) : a.v_reset) : hm;
+        if (i < a.N && dd < a.d) ot[i * a.o_row] = sp ? 0x3F80u : 0u;
+      }
+      if (a.o_counts) {
+        int32_t* oc = a.o_counts + ((static_cast<int64_t>(t) * a.B * a.H + bh) * a.N) * a.d;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int i = ti * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-          const float o = static_cast<float>(acc[e]);
-          const float hm = __fadd_rn(__fmul_rn(a.decay, vm[ti][td][e]), __fmul_rn(a.in_scale, o));
-          const bool s = hm >= a.vth;
-          vm[ti][td][e] = s ? (a.soft_reset ? __fsub_rn(hm, a.vth) : a.v_reset) : hm;
-          if (i < a.N && dd < a.d) {
-            const int64_t row = static_cast<int64_t>(b) * a.N + i;
-            a.out[static_cast<int64_t>(t) * a.o_t + row * a.o_row + h * a.d + dd] = s ? 0x3F80u : 0u;
-            if (a.o_counts)
-              a.o_counts[((static_cast<int64_t>(t) * a.B * a.H + bh) * a.N + i) * a.d + dd] = acc[e];
-          }
+          const int i = oi * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+          if (i < a.N && dd < a.d) oc[i * a.d + dd] = acc[e];
         }
       }
     }
@@ -160,7 +188,11 @@ extern "C" int snnk_spike_attention(const uint16_t* q, const uint16_t* k, const 
   if (T < 0 || B < 0 || H <= 0 || N < 0 || d <= 0) return SNNK_EINVAL;
   if (T == 0 || B == 0 || N == 0) return SNNK_OK;
   if (q == nullptr || k == nullptr || v == nullptr || spikes_out == nullptr) return SNNK_EINVAL;
-  if (N > kMaxTok || d > kMaxDim) return SNNK_EUNSUPPORTED;
+  if (N > kMaxTok || d > kMaxDim || d % 8 != 0) return SNNK_EUNSUPPORTED;
+  // 16-byte chunk loads: every row start and head offset on a 16-byte boundary
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || q_row % 8 || k_row % 8 ||
+      v_row % 8 || q_step % 8 || k_step % 8 || v_step % 8)
+    return SNNK_EALIGN;
   if (q_row < H * d || k_row < H * d || v_row < H * d || out_row < H * d) return SNNK_EINVAL;
   if (B * H > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
   AttnArgs a{};
@@ -175,9 +207,9 @@ extern "C" int snnk_spike_attention(const uint16_t* q, const uint16_t* k, const 
   a.soft_reset = soft_reset ? 1 : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nt = N > 32 ? 2 : 1, dt = d > 32 ? 2 : 1;
-  if (nt == 1 && dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 1>), dim3(B * H), dim3(64), 0, s, a);
-  else if (nt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 2>), dim3(B * H), dim3(64), 0, s, a);
-  else if (dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<2, 1>), dim3(B * H), dim3(64), 0, s, a);
-  else hipLaunchKernelGGL((ssa_attention_kernel<2, 2>), dim3(B * H), dim3(64), 0, s, a);
+  if (nt == 1 && dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 1>), dim3(B * H), dim3(256), 0, s, a);
+  else if (nt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 2>), dim3(B * H), dim3(256), 0, s, a);
+  else if (dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<2, 1>), dim3(B * H), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((ssa_attention_kernel<2, 2>), dim3(B * H), dim3(256), 0, s, a);
   return launch_status();
 }

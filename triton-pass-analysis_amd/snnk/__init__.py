@@ -6,14 +6,17 @@ backed by hand-written HIP kernels in ``libsnnk.so`` behind a C ABI
 (``include/snnk.h``).  There is no fallback: an operator whose library is
 missing raises.
 """
-from .kernels import (
-    if_lif, pack_bits, binary_gemm, spike_ktv_popcount, HAS_POPC,
-    fused_bias_if_lif, fused_bias_if_lif_rate, fused_bias_if_lif_stateful,
-    conv_neuron, linear_neuron, conv_bn_neuron, fold_conv_bn,
+from .kernels import *  # noqa: F401,F403
+from .kernels import __all__ as _kernels_all
+from .nn import (  # noqa: F401
+    IFNode, LIFNode, StatefulLIFNode, RateCodedLIFNode, RateCodedIFNode,
+    FusedConvNeuron, FusedLinearNeuron, FusedConvBNNeuron, FusedConvBNAddNeuron,
+    FusedAddNeuron, FusedConvBNLIFPool,
 )
+from .nn.attention import FusedSpikeAttention  # noqa: F401
 
-__all__ = [
-    "if_lif", "pack_bits", "binary_gemm", "spike_ktv_popcount", "HAS_POPC",
-    "fused_bias_if_lif", "fused_bias_if_lif_rate", "fused_bias_if_lif_stateful",
-    "conv_neuron", "linear_neuron", "conv_bn_neuron", "fold_conv_bn",
+__all__ = list(_kernels_all) + [
+    "IFNode", "LIFNode", "StatefulLIFNode", "RateCodedLIFNode", "RateCodedIFNode",
+    "FusedConvNeuron", "FusedLinearNeuron", "FusedConvBNNeuron", "FusedConvBNAddNeuron",
+    "FusedAddNeuron", "FusedConvBNLIFPool", "FusedSpikeAttention",
 ]
