@@ -54,6 +54,8 @@ SHAPES = [  # T, B, Cin, Cout, H, W, tile
     (4, 2, 32, 64, 8, 8, -1), (4, 2, 64, 64, 8, 8, 1), (3, 2, 32, 128, 8, 8, 2),
     (5, 1, 64, 256, 8, 8, 0), (4, 2, 128, 128, 4, 4, 3), (6, 1, 64, 96, 6, 6, 4),
     (1, 3, 32, 32, 4, 6, 5), (8, 1, 32, 64, 4, 4, 4), (4, 3, 64, 128, 10, 6, 2),
+    (4, 2, 64, 64, 4, 4, 6), (3, 2, 64, 96, 4, 4, 7), (4, 1, 128, 160, 4, 4, 8),
+    (5, 2, 64, 128, 8, 8, 9), (4, 2, 32, 64, 8, 8, 10), (2, 2, 64, 32, 4, 4, 11),
 ]
 
 

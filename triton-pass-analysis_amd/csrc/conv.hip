@@ -38,7 +38,12 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kKS = 32;           // K per stage
-constexpr int kRow = kKS + 8;     // LDS row pitch in bf16 (80 B: conflict-free b128 reads)
+constexpr int kRow = kKS;         // LDS row pitch in bf16 (64 B, four 16-byte chunks)
+
+// 16-byte chunk c of LDS row r is stored at chunk c ^ ((r >> 1) & 3): the
+// staging writes (two rows x four chunks per 8 lanes) and the fragment reads
+// (eight rows, one chunk per 8 lanes) then touch distinct bank groups.
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 3); }
 
 enum { MODE_LIF = 0, MODE_PREACT = 1 };
 
@@ -149,7 +154,7 @@ void conv3x3_kernel(ConvArgs a) {
     a_t[i] = t;
     a_ok[i] = ok;
     a_kg[i] = g;
-    a_lds[i] = (g * C::BM + r) * kRow + part * 8;
+    a_lds[i] = (g * C::BM + r) * kRow + swz(r, part) * 8;
   }
   int b_off[C::kBPer], b_kg[C::kBPer], b_lds[C::kBPer];
   bool b_ok[C::kBPer];
@@ -162,7 +167,7 @@ void conv3x3_kernel(ConvArgs a) {
     b_ok[i] = n0 + n < a.Cout;
     b_off[i] = (b_ok[i] ? (n0 + n) : 0) * K + part * 8;
     b_kg[i] = g;
-    b_lds[i] = (g * C::BN + n) * kRow + part * 8;
+    b_lds[i] = (g * C::BN + n) * kRow + swz(n, part) * 8;
   }
 
   const int n_stages_g = (a.n_stages + KSPLIT - 1) / KSPLIT;
@@ -243,13 +248,15 @@ void conv3x3_kernel(ConvArgs a) {
       const uint16_t* sb = ldsB + buf * C::kLdsB + (kg * C::BN + wn * TN * 32 + r_lane) * kRow;
 #pragma unroll
       for (int kk = 0; kk < kKS / 16; ++kk) {
+        // tile rows start at multiples of 32, so the swizzle depends on r_lane only
+        const int ch = swz(r_lane, kk * 2 + g_lane) * 8;
         bf16x8 fa[TM], fb[TN];
 #pragma unroll
         for (int i = 0; i < TM; ++i)
-          fa[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kRow + kk * 16 + g_lane * 8);
+          fa[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kRow + ch);
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          fb[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRow + kk * 16 + g_lane * 8);
+          fb[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRow + ch);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -371,6 +378,12 @@ int dispatch(const ConvArgs& a, int tile_hint, hipStream_t s) {
     case 3: return launch_cfg<2, 2, 1, 2, 1, POOL, MODE, TAPS>(a, s);
     case 4: return launch_cfg<1, 1, 1, 1, 4, POOL, MODE, TAPS>(a, s);
     case 5: return launch_cfg<1, 2, 1, 2, 2, POOL, MODE, TAPS>(a, s);
+    case 6: return launch_cfg<1, 1, 1, 1, 8, POOL, MODE, TAPS>(a, s);   // 32 x 32, split-K 8
+    case 7: return launch_cfg<1, 1, 1, 2, 4, POOL, MODE, TAPS>(a, s);   // 32 x 64, split-K 4
+    case 8: return launch_cfg<1, 2, 1, 2, 4, POOL, MODE, TAPS>(a, s);   // 32 x 128, split-K 4
+    case 9: return launch_cfg<2, 2, 2, 2, 2, POOL, MODE, TAPS>(a, s);   // 128 x 128, split-K 2
+    case 10: return launch_cfg<4, 1, 1, 2, 1, POOL, MODE, TAPS>(a, s);  // 128 x 64
+    case 11: return launch_cfg<1, 1, 1, 1, 16, POOL, MODE, TAPS>(a, s); // 32 x 32, split-K 16
     default: return SNNK_EINVAL;
   }
 }
