@@ -358,18 +358,22 @@ int launch_cfg(const ConvArgs& a, hipStream_t stream) {
   return launch_status();
 }
 
-// Tile shape by problem size: enough blocks for 256 CUs, big tiles when M
-// allows, split-K when M*N is small.
+// Tile shape by problem size (rows = output rows of one 4-step chunk, K =
+// 9*Cin or the Linear depth), from a sweep of every config over the VGG16 and
+// SSA layer shapes on MI355X: big tiles while M fills 256 CUs, split-K wave
+// groups as M shrinks and K grows.
 template <bool POOL, int MODE, int TAPS>
 int dispatch(const ConvArgs& a, int tile_hint, hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(a.n_quads) * 16;  // per T-chunk
+  const int64_t K = static_cast<int64_t>(a.n_stages) * kKS;
   int cfg = tile_hint;
   if (cfg < 0) {
-    if (a.Cout >= 256 && rows >= 128 * 256) cfg = 0;          // 128 x 256
-    else if (a.Cout <= 64) cfg = 1;                            // 256 x 64
-    else if (rows >= 128 * 256 / (a.Cout >= 256 ? 2 : 1)) cfg = 2;  // 128 x 128
-    else if (rows >= 64 * 128) cfg = 3;                        // 64 x 128
-    else cfg = 4;                                              // 32 x 32, split-K 4
+    if (rows >= 65536) cfg = 10;                       // 128 x 64
+    else if (rows >= 32768) cfg = a.Cout >= 256 ? 2 : 9;  // 128 x 128 (split-K 2)
+    else if (rows >= 8192) cfg = K <= 512 ? 10 : 8;    // 128 x 64 / 32 x 128 split-K 4
+    else if (rows >= 2048) cfg = K <= 2304 ? 8 : 7;    // 32 x 128 / 32 x 64, split-K 4
+    else if (rows >= 512 || a.Cout <= 64) cfg = 11;   // 32 x 32, split-K 16
+    else cfg = K <= 1024 ? 4 : 6;                      // 32 x 32, split-K 4 / 8
   }
   switch (cfg) {
     case 0: return launch_cfg<2, 2, 2, 4, 1, POOL, MODE, TAPS>(a, s);

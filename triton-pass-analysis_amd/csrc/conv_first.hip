@@ -6,6 +6,7 @@
 // The conv output is therefore the same at every step: it is computed once
 // per (pixel, channel) in fp32 on the VALU (K = 9*Cin is far too small for
 // MFMA) and the LIF recurrence runs T times on that constant current.
+// Cout % 8 == 0 and the folded weights (9*Cin*Cout fp32) fit 64 KB of LDS.
 // Output spikes go to NHWC bf16 [T][B][H][W][Cout] for the next MFMA layer.
 //
 // snnk_to_nhwc_bf16: [N][C][HW] (fp32/bf16/f16/u8) -> [N][HW][C] bf16.
@@ -14,42 +15,70 @@
 namespace snnk {
 namespace {
 
+// One thread per output pixel and group of 8 output channels, channel group
+// fastest: the lanes of one pixel share its image reads (broadcast) and a
+// wave's spike stores are contiguous 16-byte runs.  The folded weights of all
+// output channels sit in LDS as [cin*9 + tap][Cout].
+constexpr int kImgG = 8;
+constexpr int kImgMaxLds = 64 * 1024;
+
 __global__ __launch_bounds__(256) void conv_image_lif_kernel(
     const float* __restrict__ img, const float* __restrict__ w, const float* __restrict__ bias,
-    uint16_t* __restrict__ out, int T, int B, int Cin, int H, int W, int Cout, float decay,
+    uint16_t* __restrict__ out, int T, int n_pix, int Cin, int H, int W, int Cout, float decay,
     float in_scale, float vth, float v_reset, int soft_reset) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t total = static_cast<int64_t>(B) * H * W * Cout;
-  if (idx >= total) return;
-  const int n = static_cast<int>(idx % Cout);
-  const int64_t p = idx / Cout;  // (b, y, x)
-  const int x = static_cast<int>(p % W);
-  const int y = static_cast<int>((p / W) % H);
-  const int b = static_cast<int>(p / (static_cast<int64_t>(W) * H));
-  float acc = 0.0f;
+  extern __shared__ float wl[];
+  const int K = Cin * 9;
+  for (int i = threadIdx.x; i < K * Cout; i += 256) {
+    const int k = i / Cout, n = i - k * Cout;
+    wl[i] = w[static_cast<int64_t>(n) * K + k];
+  }
+  __syncthreads();
+  const int groups = Cout / kImgG;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (gid >= static_cast<int64_t>(n_pix) * groups) return;
+  const int p = static_cast<int>(gid / groups);  // (b, y, x)
+  const int n0 = (static_cast<int>(gid) - p * groups) * kImgG;
+  const int HW = H * W;
+  const int b = p / HW;
+  const int r = p - b * HW;
+  const int y = r / W, x = r - y * W;
+
+  float acc[kImgG];
+#pragma unroll
+  for (int j = 0; j < kImgG; ++j) acc[j] = 0.0f;
   for (int c = 0; c < Cin; ++c) {
-    const float* ip = img + (static_cast<int64_t>(b) * Cin + c) * H * W;
-    const float* wp = w + (static_cast<int64_t>(n) * Cin + c) * 9;
+    const float* ip = img + (static_cast<int64_t>(b) * Cin + c) * HW;
 #pragma unroll
-    for (int kh = 0; kh < 3; ++kh) {
-      const int ys = y + kh - 1;
-      if (ys < 0 || ys >= H) continue;
+    for (int tap = 0; tap < 9; ++tap) {
+      const int ys = y + tap / 3 - 1, xs = x + tap % 3 - 1;
+      const float v = (ys >= 0 && ys < H && xs >= 0 && xs < W) ? ip[ys * W + xs] : 0.0f;
+      const float* wk = wl + (c * 9 + tap) * Cout + n0;
 #pragma unroll
-      for (int kw = 0; kw < 3; ++kw) {
-        const int xs = x + kw - 1;
-        if (xs < 0 || xs >= W) continue;
-        acc = __fadd_rn(acc, __fmul_rn(ip[ys * W + xs], wp[kh * 3 + kw]));
-      }
+      for (int j = 0; j < kImgG; ++j) acc[j] = __builtin_fmaf(v, wk[j], acc[j]);
     }
   }
-  const float u = bias ? __fadd_rn(acc, bias[n]) : acc;
-  float v = 0.0f;
-  const int64_t step = static_cast<int64_t>(B) * H * W * Cout;
+  if (bias) {
+#pragma unroll
+    for (int j = 0; j < kImgG; ++j) acc[j] += bias[n0 + j];
+  }
+
+  float v[kImgG];
+#pragma unroll
+  for (int j = 0; j < kImgG; ++j) v[j] = 0.0f;
+  const int64_t step = static_cast<int64_t>(n_pix) * Cout;
+  uint16_t* o = out + static_cast<int64_t>(p) * Cout + n0;
   for (int t = 0; t < T; ++t) {
-    const float h = __fadd_rn(__fmul_rn(decay, v), __fmul_rn(in_scale, u));
-    const bool s = h >= vth;
-    v = s ? (soft_reset ? __fsub_rn(h, vth) : v_reset) : h;
-    out[t * step + idx] = s ? 0x3F80u : 0u;
+    uint32_t bits[kImgG / 2];
+#pragma unroll
+    for (int j = 0; j < kImgG; ++j) {
+      const float h = __fadd_rn(__fmul_rn(decay, v[j]), __fmul_rn(in_scale, acc[j]));
+      const bool s = h >= vth;
+      v[j] = s ? (soft_reset ? __fsub_rn(h, vth) : v_reset) : h;
+      const uint32_t sb = s ? 0x3F80u : 0u;
+      if (j & 1) bits[j / 2] |= sb << 16;
+      else bits[j / 2] = sb;
+    }
+    *reinterpret_cast<u32x4*>(o + t * step) = u32x4{bits[0], bits[1], bits[2], bits[3]};
   }
 }
 
@@ -106,17 +135,23 @@ extern "C" int snnk_conv3x3_image_lif(const float* image, const float* w, const 
   if (T < 0 || B < 0 || Cin <= 0 || H < 0 || W < 0 || Cout <= 0) return SNNK_EINVAL;
   if (T == 0 || B == 0 || H == 0 || W == 0) return SNNK_OK;
   if (image == nullptr || w == nullptr || spikes_out == nullptr) return SNNK_EINVAL;
-  if (B * H * W * Cout * T > (1ll << 40) || H > 0x7FFFFFFF || W > 0x7FFFFFFF ||
-      Cin > 4096 || Cout > 0x7FFFFFFF)
+  // channel groups of 8 are stored as 16-byte vectors; all folded weights
+  // must fit the kernel's LDS
+  const int64_t lds = Cin * 9 * Cout * 4;
+  if (Cout % kImgG != 0 || lds > kImgMaxLds) return SNNK_EUNSUPPORTED;
+  if (B * H * W > 0x7FFFFFFFll || B * H * W * Cin > (1ll << 40) ||
+      T * B * H * W * Cout > (1ll << 40))
     return SNNK_EUNSUPPORTED;
-  const int64_t total = B * H * W * Cout;
-  const int64_t blocks = (total + 255) / 256;
+  if (!aligned(spikes_out, 16)) return SNNK_EALIGN;
+  const int64_t n_pix = B * H * W;
+  const int64_t blocks = (n_pix * (Cout / kImgG) + 255) / 256;
   if (blocks > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
-  hipLaunchKernelGGL(conv_image_lif_kernel, dim3(blocks), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), image, w, bias, spikes_out,
-                     static_cast<int>(T), static_cast<int>(B), static_cast<int>(Cin),
-                     static_cast<int>(H), static_cast<int>(W), static_cast<int>(Cout), decay,
-                     in_scale, v_threshold, v_reset, soft_reset ? 1 : 0);
+  hipLaunchKernelGGL(conv_image_lif_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256),
+                     static_cast<unsigned>(lds), static_cast<hipStream_t>(stream), image, w,
+                     bias, spikes_out, static_cast<int>(T), static_cast<int>(n_pix),
+                     static_cast<int>(Cin), static_cast<int>(H), static_cast<int>(W),
+                     static_cast<int>(Cout), decay, in_scale, v_threshold, v_reset,
+                     soft_reset ? 1 : 0);
   return launch_status();
 }
 

@@ -267,10 +267,17 @@ class FusedVGGSNN(nn.Module):
         return y[:, :B, :self.num_classes]
 
     @torch.no_grad()
-    def capture(self, B: int, H: int = 32, W: int = 32, device=None):
-        """Record forward for batch B in a HIP graph; returns (graph, in, out)."""
+    def capture(self, B: int, H: int = 32, W: int = 32, device=None, x_in=None):
+        """Record forward for batch B in a HIP graph; returns (graph, in, out).
+
+        ``x_in`` (optional, fp32 contiguous [B, 3, H, W]) becomes the graph's
+        input buffer; by default a new one is allocated and the graph is kept
+        for :meth:`run_graph`."""
         device = device or self.w0.device
-        x_in = torch.zeros(B, 3, H, W, device=device)
+        keep = x_in is None
+        if keep:
+            x_in = torch.zeros(B, 3, H, W, device=device)
+        assert x_in.shape == (B, 3, H, W) and x_in.dtype == torch.float32 and x_in.is_contiguous()
         stream = torch.cuda.Stream(device)
         stream.wait_stream(torch.cuda.current_stream(device))
         with torch.cuda.stream(stream):
@@ -280,7 +287,8 @@ class FusedVGGSNN(nn.Module):
                 y = self.forward(x_in)
         torch.cuda.current_stream(device).wait_stream(stream)
         torch.cuda.synchronize(device)
-        self._graphs[(B, H, W)] = (graph, x_in, y)
+        if keep:
+            self._graphs[(B, H, W)] = (graph, x_in, y)
         return graph, x_in, y
 
     @torch.no_grad()
