@@ -37,13 +37,30 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kKS = 32;           // K per stage
-constexpr int kRow = kKS;         // LDS row pitch in bf16 (64 B, four 16-byte chunks)
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// 16-byte chunk c of LDS row r is stored at chunk c ^ ((r >> 1) & 3): the
-// staging writes (two rows x four chunks per 8 lanes) and the fragment reads
-// (eight rows, one chunk per 8 lanes) then touch distinct bank groups.
-__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 3); }
+constexpr int kKS = 64;           // K per stage
+constexpr int kRow = kKS;         // LDS row pitch in bf16 (128 B, eight 16-byte chunks)
+constexpr int kRowBytes = kRow * 2;
+constexpr int kDmaRows = 1024 / kRowBytes;  // rows filled by one wave-wide 16-byte load
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
+constexpr uint32_t kOOB = 0xFFFFFFF0u;  // buffer offset past every operand (reads zeros)
+
+// Wait until at most N of this wave's vector-memory loads are outstanding,
+// then meet the other waves of the block.  Written out so that no release
+// fence (and its full vmcnt(0) wait) is attached to the barrier.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// 16-byte chunk c of LDS row r is stored at chunk c ^ key(r).  gfx950 serves
+// a ds_read_b128 16 lanes per pass over 64 four-byte banks; the fragment
+// reads (16 consecutive rows, one chunk column) then hit 16 distinct 16-byte
+// bank groups, and the key is also conflict-free for 8-lane passes.  It
+// depends on row bits 0-3 only, so 32-row fragment tiles share it.
+__device__ __forceinline__ int swz_key(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
+__device__ __forceinline__ int swz(int r, int c) { return c ^ swz_key(r); }
 
 enum { MODE_LIF = 0, MODE_PREACT = 1 };
 
@@ -57,30 +74,37 @@ struct ConvArgs {
   int n_quads;        // quads in one time step
   int n_stages;       // K / 32
   FastDiv div_cin;
-  int64_t x_tstride;  // B*H*W*Cin
-  int64_t o_tstride;  // B*Ho*Wo*Cout
+  uint32_t x_tstride_b;  // bytes of one input step (B*H*W*Cin*2)
+  uint32_t x_bytes;      // bytes of x (T steps), below kOOB
+  uint32_t w_bytes;      // bytes of w, below kOOB
+  int64_t o_tstride;     // B*Ho*Wo*Cout
   float decay, in_scale, vth, v_reset;
   int soft_reset;
 };
 
-template <int WM, int WN, int TM, int TN, int KSPLIT, bool POOL, int MODE>
+template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF>
 struct Cfg {
   static constexpr int kWaves = WM * WN * KSPLIT;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int BM = WM * TM * 32;
   static constexpr int BN = WN * TN * 32;
   static constexpr int kQuads = BM / 16;                    // quads per block
-  static constexpr int kAChunks = KSPLIT * BM * (kKS / 8);  // 16-byte chunks
-  static constexpr int kBChunks = KSPLIT * BN * (kKS / 8);
-  static_assert(kAChunks % kThreads == 0, "A chunks must split evenly");
-  static_assert(kBChunks % kThreads == 0, "B chunks must split evenly");
-  static constexpr int kAPer = kAChunks / kThreads;
-  static constexpr int kBPer = kBChunks / kThreads;
-  static constexpr int kLdsA = KSPLIT * BM * kRow;  // bf16 elements per buffer
-  static constexpr int kLdsB = KSPLIT * BN * kRow;
-  static constexpr int kLdsBytes = 2 * (kLdsA + kLdsB) * 2;
+  // operand stages arrive by 16-byte direct-to-LDS loads, one wave-wide
+  // load filling kDmaRows rows (1 KB); the WM*WN waves of a K group share them
+  static constexpr int kSegA = BM / kDmaRows;
+  static constexpr int kSegB = BN / kDmaRows;
+  static constexpr int kGroupWaves = WM * WN;
+  static_assert(kSegA % kGroupWaves == 0 && kSegB % kGroupWaves == 0,
+                "segments must split evenly over a group's waves");
+  static constexpr int kAPer = kSegA / kGroupWaves;  // per wave: A segments first,
+  static constexpr int kBPer = kSegB / kGroupWaves;  // then B segments
+  static constexpr int kSegPer = kAPer + kBPer;
+  static constexpr int kStageBytes = KSPLIT * (BM + BN) * kRowBytes;
+  static constexpr int kBuf = NBUF;  // ring of operand stages in LDS
+  static constexpr int kLdsBytes = kBuf * kStageBytes;
   static constexpr int kRedBytes = (KSPLIT - 1) * WM * WN * TM * TN * 16 * 64 * 4;
   static constexpr int kSmem = kLdsBytes > kRedBytes ? kLdsBytes : kRedBytes;
+  static_assert(NBUF >= 2 && kSmem <= 160 * 1024, "LDS ring must fit 160 KB");
 };
 
 __device__ __forceinline__ uint16_t spike_bf16(bool s) { return s ? 0x3F80u : 0u; }
@@ -92,16 +116,15 @@ __device__ __forceinline__ int tap_dy(int tap) { return TAPS == 9 ? tap / 3 - 1 
 template <int TAPS>
 __device__ __forceinline__ int tap_dx(int tap) { return TAPS == 9 ? tap % 3 - 1 : 0; }
 
-template <int WM, int WN, int TM, int TN, int KSPLIT, bool POOL, int MODE, int TAPS>
+template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int MODE, int TAPS>
 __global__ __launch_bounds__(64 * WM * WN * KSPLIT)
 void conv3x3_kernel(ConvArgs a) {
-  using C = Cfg<WM, WN, TM, TN, KSPLIT, POOL, MODE>;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[C::kSmem];
-  uint16_t* ldsA = reinterpret_cast<uint16_t*>(smem);          // [2][KS][BM][kRow]
-  uint16_t* ldsB = ldsA + 2 * C::kLdsA;                        // [2][KS][BN][kRow]
+  using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF>;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::kSmem];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kg = wave / (WM * WN);
   const int wmn = wave - kg * (WM * WN);
   const int wm = wmn / WN, wn = wmn - wm * WN;
@@ -110,64 +133,67 @@ void conv3x3_kernel(ConvArgs a) {
   const int HW = a.H * a.W;
   const int K = TAPS * a.Cin;
 
-  // ---- per-thread A chunk geometry (fixed for the whole kernel) ----------
-  // chunk c -> (group, row, 16-byte part); row -> (quad, pixel q, step t)
-  int a_off[C::kAPer];      // element offset of (b, y, x, part*8) in one step
-  int a_t[C::kAPer];        // step within the chunk of 4
-  uint32_t a_ok[C::kAPer];  // bit tap: source pixel inside the image; bit 9: row valid
-  int a_kg[C::kAPer];
-  int a_lds[C::kAPer];      // LDS element offset inside a buffer
+  // Operands are read through range-checked buffer descriptors: an offset
+  // at or past the end returns zeros, which is how padding taps, rows past
+  // the last pixel, steps past T and columns past Cout are filled.
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), 0, a.x_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t wr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.w), 0, a.w_bytes, kRsrcWord3);
+
+  // ---- segment geometry (fixed for the whole kernel) ----------------------
+  // A segment q of a group's stage is A rows kDmaRows*q.. (1 KB), B segment
+  // q is B rows kDmaRows*q..; wave wmn of the group loads A segments
+  // wmn + i*kGroupWaves (i < kAPer) and the same B segments (i < kBPer).
+  // Lane l writes row kDmaRows*q + l/8, chunk slot l%8, and so reads source
+  // chunk c = slot ^ key(row).  Chunks 0-3 hold k0..k0+31 of the stage, chunks 4-7
+  // k0+32..k0+63; with Cin % 64 == 32 the halves may fall in different taps.
+  const int lrow = lane >> 3, slot = lane & 7;
+  uint32_t s_base[C::kSegPer];  // A: bytes of (t, b, y, x, chunk % 4); B: bytes of (n, chunk)
+  uint32_t s_mask[C::kSegPer];  // A: bit tap = source pixel in the image, bit 31 = upper half;
+                                // B: bit 0 = n < Cout, bits 4-6 = chunk
 #pragma unroll
-  for (int i = 0; i < C::kAPer; ++i) {
-    const int c = tid + i * C::kThreads;
-    const int g = c / (C::BM * 4);
-    const int rem = c - g * (C::BM * 4);
-    const int r = rem >> 2, part = rem & 3;
-    const int rr = r & 31;
-    const int q = rr >> 3, gr = (rr >> 2) & 1, t = rr & 3;
-    const int quad = quad0 + (r >> 5) * 2 + gr;
-    int b = 0, y = 0, xx = 0;
-    const bool row_ok = quad < a.n_quads;
-    if (row_ok) {
-      if constexpr (POOL) {
-        const int howo = a.Ho * a.Wo;
-        b = quad / howo;
-        const int r2 = quad - b * howo;
-        const int py = r2 / a.Wo, px = r2 - py * a.Wo;
-        y = 2 * py + (q >> 1);
-        xx = 2 * px + (q & 1);
-      } else {
-        const int p = quad * 4 + q;
-        b = p / HW;
-        const int r2 = p - b * HW;
-        y = r2 / a.W;
-        xx = r2 - y * a.W;
+  for (int i = 0; i < C::kSegPer; ++i) {
+    if (i < C::kAPer) {
+      const int q = wmn + i * C::kGroupWaves;
+      const int r = kDmaRows * q + lrow;
+      const int rr = r & 31;
+      const int pq = rr >> 3, gr = (rr >> 2) & 1, t = rr & 3;
+      const int quad = quad0 + (r >> 5) * 2 + gr;
+      int b = 0, y = 0, xx = 0;
+      const bool row_ok = quad < a.n_quads;
+      if (row_ok) {
+        if constexpr (POOL) {
+          const int howo = a.Ho * a.Wo;
+          b = quad / howo;
+          const int r2 = quad - b * howo;
+          const int py = r2 / a.Wo, px = r2 - py * a.Wo;
+          y = 2 * py + (pq >> 1);
+          xx = 2 * px + (pq & 1);
+        } else {
+          const int p = quad * 4 + pq;
+          b = p / HW;
+          const int r2 = p - b * HW;
+          y = r2 / a.W;
+          xx = r2 - y * a.W;
+        }
       }
-    }
-    uint32_t ok = row_ok ? (1u << 9) : 0u;
+      uint32_t ok = 0;
 #pragma unroll
-    for (int tap = 0; tap < TAPS; ++tap) {
-      const int ys = y + tap_dy<TAPS>(tap), xs = xx + tap_dx<TAPS>(tap);
-      if (row_ok && ys >= 0 && ys < a.H && xs >= 0 && xs < a.W) ok |= 1u << tap;
+      for (int tap = 0; tap < TAPS; ++tap) {
+        const int ys = y + tap_dy<TAPS>(tap), xs = xx + tap_dx<TAPS>(tap);
+        if (row_ok && ys >= 0 && ys < a.H && xs >= 0 && xs < a.W) ok |= 1u << tap;
+      }
+      const int c = swz(r, slot);
+      s_base[i] = static_cast<uint32_t>(t) * a.x_tstride_b +
+                  static_cast<uint32_t>(((b * a.H + y) * a.W + xx) * a.Cin) * 2u + (c & 3) * 16u;
+      s_mask[i] = ok | (static_cast<uint32_t>(c >> 2) << 31);
+    } else {
+      const int n = kDmaRows * (wmn + (i - C::kAPer) * C::kGroupWaves) + lrow;
+      const int c = swz(n, slot);
+      s_mask[i] = (n0 + n < a.Cout ? 1u : 0u) | (static_cast<uint32_t>(c) << 4);
+      s_base[i] = static_cast<uint32_t>(n0 + n) * static_cast<uint32_t>(K) * 2u + c * 16u;
     }
-    a_off[i] = ((b * a.H + y) * a.W + xx) * a.Cin + part * 8;
-    a_t[i] = t;
-    a_ok[i] = ok;
-    a_kg[i] = g;
-    a_lds[i] = (g * C::BM + r) * kRow + swz(r, part) * 8;
-  }
-  int b_off[C::kBPer], b_kg[C::kBPer], b_lds[C::kBPer];
-  bool b_ok[C::kBPer];
-#pragma unroll
-  for (int i = 0; i < C::kBPer; ++i) {
-    const int c = tid + i * C::kThreads;
-    const int g = c / (C::BN * 4);
-    const int rem = c - g * (C::BN * 4);
-    const int n = rem >> 2, part = rem & 3;
-    b_ok[i] = n0 + n < a.Cout;
-    b_off[i] = (b_ok[i] ? (n0 + n) : 0) * K + part * 8;
-    b_kg[i] = g;
-    b_lds[i] = (g * C::BN + n) * kRow + swz(n, part) * 8;
   }
 
   const int n_stages_g = (a.n_stages + KSPLIT - 1) / KSPLIT;
@@ -201,71 +227,113 @@ void conv3x3_kernel(ConvArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    u32x4 ra[C::kAPer], rb[C::kBPer];
-    auto gload = [&](int s) {
+    // steps past T read zeros
+    uint32_t live_mask[C::kSegPer];
+    const bool t_ok = tc * 4 + (lrow & 3) < a.T;
 #pragma unroll
-      for (int i = 0; i < C::kAPer; ++i) {
-        // a group whose interleaved stage runs past K loads zeros
-        const int sg = s * KSPLIT + a_kg[i];
-        const int k0 = (sg < a.n_stages ? sg : 0) * kKS;
-        const int tap = TAPS == 9 ? static_cast<int>(fdiv(static_cast<uint32_t>(k0), a.div_cin)) : 0;
-        const int cin0 = k0 - tap * a.Cin;
-        const int tg = tc * 4 + a_t[i];
-        u32x4 z = {0u, 0u, 0u, 0u};
-        if (((a_ok[i] >> tap) & 1u) && (a_ok[i] >> 9) && tg < a.T && sg < a.n_stages) {
-          const int dy = tap_dy<TAPS>(tap), dx = tap_dx<TAPS>(tap);
-          const int64_t off = static_cast<int64_t>(tg) * a.x_tstride + a_off[i] +
-                              (dy * a.W + dx) * a.Cin + cin0;
-          z = *reinterpret_cast<const u32x4*>(a.x + off);
-        }
-        ra[i] = z;
-      }
-#pragma unroll
-      for (int i = 0; i < C::kBPer; ++i) {
-        const int sg = s * KSPLIT + b_kg[i];
-        u32x4 z = {0u, 0u, 0u, 0u};
-        if (b_ok[i] && sg < a.n_stages)
-          z = *reinterpret_cast<const u32x4*>(a.w + b_off[i] + sg * kKS);
-        rb[i] = z;
-      }
+    for (int i = 0; i < C::kSegPer; ++i)
+      live_mask[i] = (i >= C::kAPer || t_ok) ? s_mask[i] : 0u;  // no tap bit left: zeros
+    const uint32_t chunk_off = static_cast<uint32_t>(tc) * 4u * a.x_tstride_b;
+
+    // enqueue the direct global->LDS loads of group-local stage sl
+    // wave-uniform addressing of group-local stage sl
+    struct StageAddr {
+      bool live;
+      int tap_lo, tap_hi, k_left;
+      uint32_t d_lo, d_hi, b_delta;
     };
-    auto lstore = [&](int buf) {
-#pragma unroll
-      for (int i = 0; i < C::kAPer; ++i)
-        *reinterpret_cast<u32x4*>(ldsA + buf * C::kLdsA + a_lds[i]) = ra[i];
-#pragma unroll
-      for (int i = 0; i < C::kBPer; ++i)
-        *reinterpret_cast<u32x4*>(ldsB + buf * C::kLdsB + b_lds[i]) = rb[i];
+    auto stage_addr = [&](int sl) {
+      StageAddr p;
+      const int sg = sl * KSPLIT + kg;
+      p.live = sg < a.n_stages;
+      const int k0 = p.live ? sg * kKS : 0;
+      // tap and channel offset of each 32-wide half of the stage; a half at
+      // or past K gets tap TAPS, which no source pixel mask contains
+      p.tap_lo = static_cast<int>(fdiv(static_cast<uint32_t>(k0), a.div_cin));
+      p.tap_hi = static_cast<int>(fdiv(static_cast<uint32_t>(k0 + 32), a.div_cin));
+      const int cin_lo = k0 - p.tap_lo * a.Cin, cin_hi = k0 + 32 - p.tap_hi * a.Cin;
+      p.d_lo = chunk_off + static_cast<uint32_t>(
+          ((tap_dy<TAPS>(p.tap_lo) * a.W + tap_dx<TAPS>(p.tap_lo)) * a.Cin + cin_lo) * 2);
+      p.d_hi = chunk_off + static_cast<uint32_t>(
+          ((tap_dy<TAPS>(p.tap_hi) * a.W + tap_dx<TAPS>(p.tap_hi)) * a.Cin + cin_hi) * 2);
+      p.b_delta = static_cast<uint32_t>(k0) * 2u;
+      p.k_left = K - k0;  // chunk c of a B row is inside K when 8c < k_left
+      return p;
+    };
+    // enqueue the direct global->LDS load of segment i of a stage
+    auto issue_seg = [&](const StageAddr& p, int i, int buf) {
+      unsigned char* stage = smem + buf * C::kStageBytes;
+      const uint32_t m = live_mask[i];
+      const uint32_t live = p.live ? 1u : 0u;
+      if (i < C::kAPer) {  // resolved at compile time
+        const int q = wmn + i * C::kGroupWaves;
+        const uint32_t hi = m >> 31;
+        const int tap = hi ? p.tap_hi : p.tap_lo;
+        const uint32_t ok = live & (m >> tap);
+        const uint32_t off = (ok & 1u) ? s_base[i] + (hi ? p.d_hi : p.d_lo) : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr, (lds_ptr_t)(stage + (kg * C::BM + kDmaRows * q) * kRowBytes), 16, off, 0, 0, 0);
+      } else {
+        const int q = wmn + (i - C::kAPer) * C::kGroupWaves;
+        const uint32_t in_k = static_cast<int>(8 * ((m >> 4) & 7u)) < p.k_left ? 1u : 0u;
+        const uint32_t ok = live & m & in_k;
+        const uint32_t off = (ok & 1u) ? s_base[i] + p.b_delta : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            wr, (lds_ptr_t)(stage + (KSPLIT * C::BM + kg * C::BN + kDmaRows * q) * kRowBytes),
+            16, off, 0, 0, 0);
+      }
     };
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int s = 0; s < n_stages_g; ++s) {
-      const int buf = s & 1;
-      if (s + 1 < n_stages_g) gload(s + 1);
-      const uint16_t* sa = ldsA + buf * C::kLdsA + (kg * C::BM + wm * TM * 32 + r_lane) * kRow;
-      const uint16_t* sb = ldsB + buf * C::kLdsB + (kg * C::BN + wn * TN * 32 + r_lane) * kRow;
 #pragma unroll
-      for (int kk = 0; kk < kKS / 16; ++kk) {
+    for (int p = 0; p < C::kBuf - 1; ++p) {
+      const StageAddr sp = stage_addr(p);
+#pragma unroll
+      for (int i = 0; i < C::kSegPer; ++i) issue_seg(sp, i, p);
+    }
+    constexpr int kSlices = kKS / 16;
+    int buf = 0;
+    for (int s = 0; s < n_stages_g; ++s) {
+      // this wave's loads of stage s are done once at most the later
+      // stages' loads are outstanding; the barrier publishes every wave's
+      // loads and retires the reads of the buffer refilled next
+      wait_vmcnt_barrier<C::kSegPer * (C::kBuf - 2)>();
+      const int nbuf = buf == 0 ? C::kBuf - 1 : buf - 1;
+      const StageAddr sp = stage_addr(s + C::kBuf - 1);
+      const unsigned char* st = smem + buf * C::kStageBytes;
+      const uint16_t* sa = reinterpret_cast<const uint16_t*>(st) + (kg * C::BM + wm * TM * 32 + r_lane) * kRow;
+      const uint16_t* sb = reinterpret_cast<const uint16_t*>(st) +
+                           (KSPLIT * C::BM + kg * C::BN + wn * TN * 32 + r_lane) * kRow;
+      auto read = [&](bf16x8 (&fa)[TM], bf16x8 (&fb)[TN], int kk) {
         // tile rows start at multiples of 32, so the swizzle depends on r_lane only
         const int ch = swz(r_lane, kk * 2 + g_lane) * 8;
-        bf16x8 fa[TM], fb[TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          fa[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kRow + ch);
+        for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kRow + ch);
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          fb[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRow + ch);
+        for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRow + ch);
+      };
+      // software pipeline over the k-slices: the reads of slice kk+1 and a
+      // share of the next stage's loads are in flight while slice kk's MFMAs
+      // run; the scheduling barriers keep that order
+      bf16x8 fa[2][TM], fb[2][TN];
+      read(fa[0], fb[0], 0);
+#pragma unroll
+      for (int kk = 0; kk < kSlices; ++kk) {
+        if (kk + 1 < kSlices) read(fa[(kk + 1) & 1], fb[(kk + 1) & 1], kk + 1);
+#pragma unroll
+        for (int i = 0; i < C::kSegPer; ++i)
+          if (i % kSlices == kk) issue_seg(sp, i, nbuf);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      if (s + 1 < n_stages_g) lstore(buf ^ 1);
-      __syncthreads();
+      buf = buf + 1 == C::kBuf ? 0 : buf + 1;
     }
+    // the trailing loads (zero fills of unused buffers) land before LDS is reused
+    wait_vmcnt_barrier<0>();
 
     // ---- split-K reduction through LDS ----------------------------------
     if constexpr (KSPLIT > 1) {
@@ -348,19 +416,20 @@ void conv3x3_kernel(ConvArgs a) {
   }
 }
 
-template <int WM, int WN, int TM, int TN, int KSPLIT, bool POOL, int MODE, int TAPS>
+template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int MODE, int TAPS>
 int launch_cfg(const ConvArgs& a, hipStream_t stream) {
-  using C = Cfg<WM, WN, TM, TN, KSPLIT, POOL, MODE>;
+  using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF>;
   const int gx = (a.n_quads + C::kQuads - 1) / C::kQuads;
   const int gy = (a.Cout + C::BN - 1) / C::BN;
-  hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, POOL, MODE, TAPS>), dim3(gx, gy),
+  hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, NBUF, POOL, MODE, TAPS>), dim3(gx, gy),
                      dim3(C::kThreads), 0, stream, a);
   return launch_status();
 }
 
+constexpr int kNumTiles = 19;
+
 // Tile shape by problem size (rows = output rows of one 4-step chunk, K =
-// 9*Cin or the Linear depth), from a sweep of every config over the VGG16 and
-// SSA layer shapes on MI355X: big tiles while M fills 256 CUs, split-K wave
+// 9*Cin or the Linear depth): big tiles while M fills 256 CUs, split-K wave
 // groups as M shrinks and K grows.
 template <bool POOL, int MODE, int TAPS>
 int dispatch(const ConvArgs& a, int tile_hint, hipStream_t s) {
@@ -368,26 +437,36 @@ int dispatch(const ConvArgs& a, int tile_hint, hipStream_t s) {
   const int64_t K = static_cast<int64_t>(a.n_stages) * kKS;
   int cfg = tile_hint;
   if (cfg < 0) {
-    if (rows >= 65536) cfg = 10;                       // 128 x 64
-    else if (rows >= 32768) cfg = a.Cout >= 256 ? 2 : 9;  // 128 x 128 (split-K 2)
-    else if (rows >= 8192) cfg = K <= 512 ? 10 : 8;    // 128 x 64 / 32 x 128 split-K 4
-    else if (rows >= 2048) cfg = K <= 2304 ? 8 : 7;    // 32 x 128 / 32 x 64, split-K 4
-    else if (rows >= 512 || a.Cout <= 64) cfg = 11;   // 32 x 32, split-K 16
-    else cfg = K <= 1024 ? 4 : 6;                      // 32 x 32, split-K 4 / 8
+    if (rows >= 65536) cfg = 1;                                        // 256 x 64
+    else if (rows >= 32768) cfg = a.Cout >= 256 ? 14 : (K <= 576 ? 3 : 9);
+    else if (rows >= 8192) cfg = 3;                                    // 64 x 128
+    else if (rows >= 2048) cfg = 8;                                    // 32 x 128 split-K 4
+    else if (rows >= 512) cfg = 4;                                     // 32 x 32 split-K 4
+    else if (a.Cout <= 64) cfg = 6;                                    // 32 x 32 split-K 8
+    else if (K <= 1024) cfg = 7;                                       // 32 x 64 split-K 4
+    else cfg = rows >= 128 ? 13 : 4;
   }
+  //                               WM WN TM TN KS NBUF           block tile, LDS
   switch (cfg) {
-    case 0: return launch_cfg<2, 2, 2, 4, 1, POOL, MODE, TAPS>(a, s);
-    case 1: return launch_cfg<4, 1, 2, 2, 1, POOL, MODE, TAPS>(a, s);
-    case 2: return launch_cfg<2, 2, 2, 2, 1, POOL, MODE, TAPS>(a, s);
-    case 3: return launch_cfg<2, 2, 1, 2, 1, POOL, MODE, TAPS>(a, s);
-    case 4: return launch_cfg<1, 1, 1, 1, 4, POOL, MODE, TAPS>(a, s);
-    case 5: return launch_cfg<1, 2, 1, 2, 2, POOL, MODE, TAPS>(a, s);
-    case 6: return launch_cfg<1, 1, 1, 1, 8, POOL, MODE, TAPS>(a, s);   // 32 x 32, split-K 8
-    case 7: return launch_cfg<1, 1, 1, 2, 4, POOL, MODE, TAPS>(a, s);   // 32 x 64, split-K 4
-    case 8: return launch_cfg<1, 2, 1, 2, 4, POOL, MODE, TAPS>(a, s);   // 32 x 128, split-K 4
-    case 9: return launch_cfg<2, 2, 2, 2, 2, POOL, MODE, TAPS>(a, s);   // 128 x 128, split-K 2
-    case 10: return launch_cfg<4, 1, 1, 2, 1, POOL, MODE, TAPS>(a, s);  // 128 x 64
-    case 11: return launch_cfg<1, 1, 1, 1, 16, POOL, MODE, TAPS>(a, s); // 32 x 32, split-K 16
+    case 0: return launch_cfg<2, 2, 2, 4, 1, 3, POOL, MODE, TAPS>(a, s);   // 128 x 256, 144 KB
+    case 1: return launch_cfg<4, 1, 2, 2, 1, 2, POOL, MODE, TAPS>(a, s);   // 256 x 64, 80 KB
+    case 2: return launch_cfg<2, 2, 2, 2, 1, 2, POOL, MODE, TAPS>(a, s);   // 128 x 128, 64 KB
+    case 3: return launch_cfg<2, 2, 1, 2, 1, 3, POOL, MODE, TAPS>(a, s);   // 64 x 128, 72 KB
+    case 4: return launch_cfg<1, 1, 1, 1, 4, 3, POOL, MODE, TAPS>(a, s);   // 32 x 32 split-K 4, 96 KB
+    case 5: return launch_cfg<1, 2, 1, 2, 2, 2, POOL, MODE, TAPS>(a, s);   // 32 x 128 split-K 2, 80 KB
+    case 6: return launch_cfg<1, 1, 1, 1, 8, 2, POOL, MODE, TAPS>(a, s);   // 32 x 32 split-K 8, 128 KB
+    case 7: return launch_cfg<1, 1, 1, 2, 4, 2, POOL, MODE, TAPS>(a, s);   // 32 x 64 split-K 4, 96 KB
+    case 8: return launch_cfg<1, 2, 1, 2, 4, 2, POOL, MODE, TAPS>(a, s);   // 32 x 128 split-K 4, 160 KB
+    case 9: return launch_cfg<2, 2, 2, 2, 2, 2, POOL, MODE, TAPS>(a, s);   // 128 x 128 split-K 2, 128 KB
+    case 10: return launch_cfg<4, 1, 1, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 128 x 64, 72 KB
+    case 11: return launch_cfg<2, 2, 2, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 128 x 128, 96 KB
+    case 12: return launch_cfg<4, 1, 1, 2, 1, 4, POOL, MODE, TAPS>(a, s);  // 128 x 64, 96 KB
+    case 13: return launch_cfg<1, 1, 1, 2, 2, 3, POOL, MODE, TAPS>(a, s);  // 32 x 64 split-K 2, 72 KB
+    case 14: return launch_cfg<4, 2, 2, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 256 x 128, 144 KB
+    case 15: return launch_cfg<2, 2, 2, 2, 1, 4, POOL, MODE, TAPS>(a, s);  // 128 x 128, 128 KB
+    case 16: return launch_cfg<2, 2, 1, 2, 1, 4, POOL, MODE, TAPS>(a, s);  // 64 x 128, 96 KB
+    case 17: return launch_cfg<4, 1, 1, 2, 1, 5, POOL, MODE, TAPS>(a, s);  // 128 x 64, 120 KB
+    case 18: return launch_cfg<1, 2, 1, 2, 2, 3, POOL, MODE, TAPS>(a, s);  // 32 x 128 split-K 2, 120 KB
     default: return SNNK_EINVAL;
   }
 }
@@ -410,13 +489,14 @@ extern "C" int snnk_conv3x3_bn_lif(const uint16_t* x, const uint16_t* w, const f
   const bool preact = preact_out != nullptr;
   if (!preact && spikes_out == nullptr) return SNNK_EINVAL;
   if (preact && pool) return SNNK_EINVAL;
-  if (Cin % kKS != 0 || Cout % 32 != 0) return SNNK_EUNSUPPORTED;
+  if (Cin % 32 != 0 || Cout % 32 != 0) return SNNK_EUNSUPPORTED;
+  if (tile_hint >= kNumTiles) return SNNK_EINVAL;
   if (pool && (H % 2 != 0 || W % 2 != 0)) return SNNK_EUNSUPPORTED;
   if (!pool && (B * H * W) % 4 != 0) return SNNK_EUNSUPPORTED;
   const int64_t step_in = B * H * W * Cin;
   const int64_t step_out = B * H * W * Cout;
-  if (T * step_in > 0x7FFFFFFFll || T * step_out > (1ll << 40) || 9 * Cin > 0x7FFFFFFF ||
-      B * H * W * Cin > 0x7FFFFFFFll || Cout * 9 * Cin > 0x7FFFFFFFll)
+  // byte offsets into x and w are 32-bit (buffer descriptors)
+  if (T * step_in * 2 > kOOB || T * step_out > (1ll << 40) || Cout * 9 * Cin * 2 > kOOB)
     return SNNK_EUNSUPPORTED;
   if (!aligned(x, 16) || !aligned(w, 16)) return SNNK_EALIGN;
 
@@ -428,9 +508,11 @@ extern "C" int snnk_conv3x3_bn_lif(const uint16_t* x, const uint16_t* w, const f
   a.Ho = pool ? a.H / 2 : a.H;
   a.Wo = pool ? a.W / 2 : a.W;
   a.n_quads = pool ? a.B * a.Ho * a.Wo : a.B * a.H * a.W / 4;
-  a.n_stages = static_cast<int>(9 * Cin / kKS);
+  a.n_stages = static_cast<int>((9 * Cin + kKS - 1) / kKS);
   a.div_cin = make_fastdiv(static_cast<uint32_t>(Cin));
-  a.x_tstride = step_in;
+  a.x_tstride_b = static_cast<uint32_t>(step_in * 2);
+  a.x_bytes = static_cast<uint32_t>(T * step_in * 2);
+  a.w_bytes = static_cast<uint32_t>(Cout * 9 * Cin * 2);
   a.o_tstride = B * a.Ho * a.Wo * Cout;
   a.decay = decay; a.in_scale = in_scale; a.vth = v_threshold; a.v_reset = v_reset;
   a.soft_reset = soft_reset ? 1 : 0;
@@ -452,9 +534,9 @@ extern "C" int snnk_linear_bias_lif(const uint16_t* x, const uint16_t* w, const 
   if (x == nullptr || w == nullptr) return SNNK_EINVAL;
   const bool preact = preact_out != nullptr;
   if (!preact && spikes_out == nullptr) return SNNK_EINVAL;
-  if (K % kKS != 0 || N % 32 != 0 || R % 4 != 0) return SNNK_EUNSUPPORTED;
-  if (T * R * K > 0x7FFFFFFFll || R * K > 0x7FFFFFFFll || N * K > 0x7FFFFFFFll ||
-      T * R * N > (1ll << 40))
+  if (K % 32 != 0 || N % 32 != 0 || R % 4 != 0) return SNNK_EUNSUPPORTED;
+  if (tile_hint >= kNumTiles) return SNNK_EINVAL;
+  if (T * R * K * 2 > kOOB || N * K * 2 > kOOB || T * R * N > (1ll << 40))
     return SNNK_EUNSUPPORTED;
   if (!aligned(x, 16) || !aligned(w, 16)) return SNNK_EALIGN;
   ConvArgs a{};
@@ -463,9 +545,11 @@ extern "C" int snnk_linear_bias_lif(const uint16_t* x, const uint16_t* w, const 
   a.Cin = static_cast<int>(K); a.Cout = static_cast<int>(N);
   a.Ho = 1; a.Wo = a.W;
   a.n_quads = static_cast<int>(R / 4);
-  a.n_stages = static_cast<int>(K / kKS);
+  a.n_stages = static_cast<int>((K + kKS - 1) / kKS);
   a.div_cin = make_fastdiv(static_cast<uint32_t>(K));
-  a.x_tstride = R * K;
+  a.x_tstride_b = static_cast<uint32_t>(R * K * 2);
+  a.x_bytes = static_cast<uint32_t>(T * R * K * 2);
+  a.w_bytes = static_cast<uint32_t>(N * K * 2);
   a.o_tstride = R * N;
   a.decay = decay; a.in_scale = in_scale; a.vth = v_threshold; a.v_reset = v_reset;
   a.soft_reset = soft_reset ? 1 : 0;
