@@ -78,6 +78,7 @@ struct ConvArgs {
   uint32_t x_bytes;      // bytes of x (T steps), below kOOB
   uint32_t w_bytes;      // bytes of w, below kOOB
   int64_t o_tstride;     // B*Ho*Wo*Cout
+  int tiles_m, tiles_n;  // output tiles along rows (quads) and Cout
   float decay, in_scale, vth, v_reset;
   int soft_reset;
 };
@@ -128,8 +129,16 @@ void conv3x3_kernel(ConvArgs a) {
   const int kg = wave / (WM * WN);
   const int wmn = wave - kg * (WM * WN);
   const int wm = wmn / WN, wn = wmn - wm * WN;
-  const int quad0 = blockIdx.x * C::kQuads;
-  const int n0 = blockIdx.y * C::BN;
+  // Workgroups are dealt to the 8 XCDs round-robin by id; id -> tile is
+  // remapped so that each XCD runs one contiguous range of tiles (row tile
+  // major, Cout tile minor) and its L2 holds only that range's activations.
+  const int n_tiles = a.tiles_m * a.tiles_n;
+  const int per_xcd = (n_tiles + 7) / 8;
+  const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (tile >= n_tiles) return;  // whole workgroup: no barrier is left waiting
+  const int tm = tile / a.tiles_n;
+  const int quad0 = tm * C::kQuads;
+  const int n0 = (tile - tm * a.tiles_n) * C::BN;
   const int HW = a.H * a.W;
   const int K = TAPS * a.Cin;
 
@@ -419,10 +428,13 @@ void conv3x3_kernel(ConvArgs a) {
 template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int MODE, int TAPS>
 int launch_cfg(const ConvArgs& a, hipStream_t stream) {
   using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF>;
-  const int gx = (a.n_quads + C::kQuads - 1) / C::kQuads;
-  const int gy = (a.Cout + C::BN - 1) / C::BN;
-  hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, NBUF, POOL, MODE, TAPS>), dim3(gx, gy),
-                     dim3(C::kThreads), 0, stream, a);
+  ConvArgs b = a;
+  b.tiles_m = (a.n_quads + C::kQuads - 1) / C::kQuads;
+  b.tiles_n = (a.Cout + C::BN - 1) / C::BN;
+  const int64_t per_xcd = (static_cast<int64_t>(b.tiles_m) * b.tiles_n + 7) / 8;
+  if (per_xcd * 8 > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
+  hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, NBUF, POOL, MODE, TAPS>),
+                     dim3(static_cast<unsigned>(per_xcd * 8)), dim3(C::kThreads), 0, stream, b);
   return launch_status();
 }
 
