@@ -374,7 +374,7 @@ def bench_vgg(args, dev):
     from oracle import vgg as ov
 
     T = 4
-    eng = vgg16_snn(num_classes=10, pool="max", input_size=32, seed=0, fused=True).to(dev)
+    eng = vgg16_snn(num_classes=10, pool="max", input_size=32, seed=0, engine=True).to(dev)
     params = ov.make_params(0)
     recs = {}
     for B in (32, 1, 56):

@@ -139,6 +139,69 @@ class _RefSSA(nn.Module):
         self.proj_conv = nn.Conv1d(C, C, 1)
         self.proj_bn = _bn1d(C, g)
 
+    def forward(self, x):
+        """Reference block forward (test_spike_attention.py:67-80)."""
+        T, B, C, H, W = x.shape
+        N, heads = H * W, self.num_heads
+        d = C // heads
+        x = self.proj_lif(x).flatten(3)
+        xf = x.flatten(0, 1)
+
+        def proj(nm):
+            y = getattr(self, f"{nm}_bn")(getattr(self, f"{nm}_conv")(xf)).reshape(T, B, C, N)
+            return _heads(getattr(self, f"{nm}_lif")(y), T, B, N, heads, d)
+        q, k, v = proj("q"), proj("k"), proj("v")
+        a = (q @ (k.transpose(-2, -1) @ v)) * self.scale
+        s = self.attn_lif(a.transpose(3, 4).reshape(T, B, C, N)).flatten(0, 1)
+        return self.proj_bn(self.proj_conv(s)).reshape(T, B, C, H, W)
+
+
+def _heads(s, T, B, N, heads, d):
+    return s.transpose(-1, -2).reshape(T, B, N, heads, d).permute(0, 1, 3, 2, 4).contiguous()
+
+
+def _bn2d(c, g):
+    bn = nn.BatchNorm2d(c).eval()
+    with torch.no_grad():
+        bn.running_mean.copy_(torch.randn(c, generator=g) * 0.2)
+        bn.running_var.copy_(torch.rand(c, generator=g) + 0.5)
+        bn.weight.copy_(torch.rand(c, generator=g) + 0.5)
+        bn.bias.copy_(torch.randn(c, generator=g) * 0.2)
+    return bn
+
+
+class _RefMS(nn.Module):
+    """Structure of snn_compiler/tests/test_spike_attention.py:83-107 (SDT-V2
+    MS_Attention with plain 3x3 convs in place of RepConv)."""
+
+    def __init__(self, C=32, heads=4, seed=1):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        self.num_heads, self.scale = heads, 0.125
+        self.head_lif = _LIF(v_threshold=0.3)
+        for nm in ("q", "k", "v", "proj"):
+            conv = nn.Conv2d(C, C, 3, padding=1, bias=False)
+            with torch.no_grad():
+                conv.weight.copy_(torch.randn(C, C, 3, 3, generator=g) * (1.0 / (9 * C)) ** 0.5)
+            setattr(self, f"{nm}_conv", nn.Sequential(conv, _bn2d(C, g)))
+        for nm in ("q", "k", "v"):
+            setattr(self, f"{nm}_lif", _LIF(v_threshold=0.3))
+        self.attn_lif = _LIF(v_threshold=0.5)
+
+    def forward(self, x):
+        T, B, C, H, W = x.shape
+        N, heads = H * W, self.num_heads
+        d = C // heads
+        x = self.head_lif(x)
+
+        def proj(nm):
+            y = getattr(self, f"{nm}_conv")(x.flatten(0, 1)).reshape(T, B, C, H, W)
+            return _heads(getattr(self, f"{nm}_lif")(y).flatten(3), T, B, N, heads, d)
+        q, k, v = proj("q"), proj("k"), proj("v")
+        a = (q @ (k.transpose(-2, -1) @ v)) * self.scale
+        s = self.attn_lif(a.transpose(3, 4).reshape(T, B, C, N)).reshape(T, B, C, H, W)
+        return self.proj_conv(s.flatten(0, 1)).reshape(T, B, C, H, W)
+
 
 def test_fused_spike_attention_from_reference_block():
     """from_reference on the reference test's block (test_spike_attention.py:110-117).
@@ -150,7 +213,7 @@ def test_fused_spike_attention_from_reference_block():
     with the fp32 block is statistical."""
     ref = _RefSSA(C=32, heads=4).eval()
     x = _spikes((4, 2, 32, 8, 8), 0.3, 0)
-    fused = FusedSpikeAttention.from_reference(ref).to(DEV)
+    fused = FusedSpikeAttention.from_reference(ref, ktv_mode="mfma").to(DEV)
     out = fused(x.to(DEV)).cpu()
     assert out.shape == x.shape
     p = {}
@@ -181,3 +244,44 @@ def test_fused_spike_attention_from_reference_block():
     ref_out = r["out"].transpose(2, 3).reshape(x.shape)
     close = ((out - ref_out).abs() < 2e-2).float().mean().item()
     assert close >= 0.95, f"fraction of close outputs {close}"
+
+
+@pytest.mark.parametrize("variant,ktv", [("ssa", "bmm"), ("ms", "bmm"), ("ssa", "popcount"),
+                                         ("ms", "popcount")])
+def test_reference_mode_bit_exact(variant, ktv):
+    """from_reference(ref, fold_bn=False) reproduces the reference block bit for
+    bit (test_spike_attention.py:110-160): the projections are the block's own
+    conv + BN, every LIF is the HIP kernel (bit-exact neuron), K^T V and
+    q (K^T V) are exact integer products and the scale folds exactly."""
+    from snnk.verify import assert_equivalent
+    ref = (_RefSSA(C=32, heads=4) if variant == "ssa" else _RefMS(C=32, heads=4)).to(DEV).eval()
+    x = _spikes((4, 2, 32, 8, 8), 0.3, 3).to(DEV)
+    fused = FusedSpikeAttention.from_reference(ref, fold_bn=False, ktv_mode=ktv).to(DEV)
+    assert fused.variant == variant and fused.ktv_mode == ktv
+    rep = assert_equivalent(ref, fused, x, verbose=False)
+    assert rep["bit_exact"]
+
+
+@pytest.mark.parametrize("variant,C,heads", [("ssa", 384, 6), ("ms", 384, 4)])
+def test_reference_mode_spikformer_shapes(variant, C, heads):
+    """Spikingformer / SDT-V2 block shapes: N = 14x14 = 196 tokens, d = 64 / 96."""
+    from snnk.verify import assert_equivalent
+    ref = (_RefSSA(C=C, heads=heads) if variant == "ssa" else _RefMS(C=C, heads=heads))
+    ref = ref.to(DEV).eval()
+    x = _spikes((4, 2, C, 14, 14), 0.2, 4).to(DEV)
+    fused = FusedSpikeAttention.from_reference(ref, fold_bn=False, ktv_mode="popcount").to(DEV)
+    rep = assert_equivalent(ref, fused, x, verbose=False)
+    assert rep["bit_exact"]
+
+
+def test_fuse_spiking_attention_pass():
+    """fuse_spiking_attention swaps both block kinds inside a container
+    (test_spike_attention.py:131-137)."""
+    from snnk.passes import fuse_spiking_attention
+    model = nn.ModuleList([_RefSSA(C=32, heads=4), _RefMS(C=32, heads=4)]).to(DEV).eval()
+    x = _spikes((4, 2, 32, 8, 8), 0.3, 5).to(DEV)
+    want = [m(x) for m in model]
+    assert fuse_spiking_attention(model, fold_bn=False) == 2
+    assert all(isinstance(m, FusedSpikeAttention) for m in model)
+    for m, y in zip(model, want):
+        assert torch.equal(m(x), y)

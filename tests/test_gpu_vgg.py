@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from oracle import vgg as ov
+from oracle import fused as of
 from snnk.kernels.conv import to_nhwc_bf16, conv3x3_image_lif
 from snnk.kernels.linear import linear_bias_lif, linear_preact
 from snnk.zoo import vgg16_snn
@@ -22,7 +23,7 @@ T = 4
 
 def _engine(gain):
     return vgg16_snn(num_classes=10, pool="max", input_size=32, seed=0, gain=gain,
-                     fused=True).to(DEV)
+                     engine=True).to(DEV)
 
 
 def _image(B, seed=1):
@@ -121,3 +122,57 @@ def test_batch_curve(B):
     ref = ov.forward(ov.make_params(0, gain=1.0), img, T)
     assert torch.equal(got.mean(0).argmax(-1), ref.mean(0).argmax(-1))
     assert ((got - ref).abs().max() / ref.abs().max()).item() < 1e-3
+
+
+def test_engine_rejects_time_varying_input():
+    eng = _engine(1.0)
+    x = torch.randn(T, 2, 3, 32, 32, device=DEV)
+    with pytest.raises(ValueError):
+        eng(x)
+    same = x[:1].expand(T, -1, -1, -1, -1).contiguous()
+    assert eng(same).shape == (T, 2, 10)
+
+
+def test_fuse_snn_model_vgg_equivalent():
+    """vgg16_snn(fused=True) = fuse_snn_model on the reference structure
+    (snn_compiler/zoo/vgg.py:134-143): every 64+-channel conv block (and its
+    max-pool) becomes one bf16-MFMA FusedConvBNLIFPool, layer 1 a
+    FusedConvBNNeuron, FC1/FC2 FusedLinearNeuron.  Checked with the verify
+    harness against the unfused model on a time-varying spike input."""
+    from snnk.verify import compare_models, assert_equivalent
+    from snnk.nn import FusedConvBNLIFPool, FusedConvBNNeuron, FusedLinearNeuron
+    ref = vgg16_snn(num_classes=10, pool="max", input_size=32, seed=0).to(DEV)
+    fused = vgg16_snn(num_classes=10, pool="max", input_size=32, seed=0, fused=True).to(DEV)
+    kinds = [type(m) for m in fused.features]
+    assert kinds.count(FusedConvBNLIFPool) == 12 and kinds.count(FusedConvBNNeuron) == 1
+    assert sum(isinstance(m, FusedLinearNeuron) for m in fused.classifier) == 2
+    assert fused._n_fused == 15
+    g = torch.Generator().manual_seed(5)
+    x = (torch.rand(T, 4, 3, 32, 32, generator=g) < 0.3).float().to(DEV)
+    rep = compare_models(ref, fused, x)
+    assert rep["shape_match"] and rep["argmax_agree"] is not None
+    # silent deep layers at gain 1: logits are the FC3 bias on both sides
+    assert_equivalent(ref, fused, x, require_bitexact=False, atol=1e-5, verbose=False)
+
+
+def test_fused_pool_module_teacher_forced():
+    """One FusedConvBNLIFPool from the pass (gain 3, active layer) against the
+    reference layers Conv2d -> BatchNorm2d -> LIFNode -> MaxPool2d fed the same
+    fp32 spike input: >= 99.9% agreement, flips only near threshold."""
+    ref = vgg16_snn(num_classes=10, pool="max", input_size=32, seed=0, gain=3.0).to(DEV)
+    fused = vgg16_snn(num_classes=10, pool="max", input_size=32, seed=0, gain=3.0,
+                      fused=True).to(DEV)
+    conv, bn, lif, pool = (ref.features[i] for i in range(3, 7))   # 64 -> 64, 32x32, pool
+    blk = fused.features[1]
+    assert blk.pool == "max"
+    g = torch.Generator().manual_seed(6)
+    x = (torch.rand(T, 4, 64, 32, 32, generator=g) < 0.2).float().to(DEV)
+    got = blk(x)
+    assert got.dtype == torch.float32
+    with torch.no_grad():
+        y = bn(conv(x.reshape(T * 4, 64, 32, 32))).view(T, 4, 64, 32, 32)
+        s = lif(y)
+        want = pool(s.reshape(T * 4, 64, 32, 32)).view(T, 4, 64, 16, 16)
+    trace = of.membrane_trace(y.cpu())
+    agree, bad = _flips_ok(got.cpu(), want.cpu(), trace, True, 5e-2)
+    assert agree >= 0.999 and not bad, agree

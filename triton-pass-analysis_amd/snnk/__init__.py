@@ -14,9 +14,12 @@ from .nn import (  # noqa: F401
     FusedAddNeuron, FusedConvBNLIFPool,
 )
 from .nn.attention import FusedSpikeAttention  # noqa: F401
+from .verify import assert_equivalent, compare_models  # noqa: F401
+from . import passes  # noqa: F401
 
 __all__ = list(_kernels_all) + [
     "IFNode", "LIFNode", "StatefulLIFNode", "RateCodedLIFNode", "RateCodedIFNode",
     "FusedConvNeuron", "FusedLinearNeuron", "FusedConvBNNeuron", "FusedConvBNAddNeuron",
     "FusedAddNeuron", "FusedConvBNLIFPool", "FusedSpikeAttention",
+    "assert_equivalent", "compare_models",
 ]

@@ -27,12 +27,13 @@ def prepare_conv3x3_weight(weight: torch.Tensor) -> torch.Tensor:
 
 def to_nhwc_bf16(x_seq: torch.Tensor) -> torch.Tensor:
     """[T, B, C, H, W] (any memory format, fp32/bf16/fp16/uint8) -> contiguous NHWC bf16
-    ``[T, B, H, W, C]``.  A bf16 channels-last input is returned as a view."""
+    ``[T, B, H, W, C]``.  A bf16 channels-last input is returned as a view, any
+    other channels-last input is cast in place of the transpose kernel."""
     assert x_seq.is_cuda and x_seq.ndim == 5, "expects a [T, B, C, H, W] GPU tensor"
     T, B, C, H, W = x_seq.shape
     nhwc = x_seq.permute(0, 1, 3, 4, 2)
-    if x_seq.dtype == torch.bfloat16 and nhwc.is_contiguous():
-        return nhwc
+    if nhwc.is_contiguous():  # channels-last memory already: a cast (RNE) or a view
+        return nhwc if x_seq.dtype == torch.bfloat16 else nhwc.to(torch.bfloat16)
     src = x_seq.contiguous()
     out = torch.empty(T, B, H, W, C, device=x_seq.device, dtype=torch.bfloat16)
     with torch.cuda.device(x_seq.device):

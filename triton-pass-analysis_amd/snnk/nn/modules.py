@@ -293,15 +293,17 @@ class FusedConvBNLIFPool(nn.Module):
     Replaces the reference's (FusedConvBNNeuron, nn.MaxPool2d) pair
     (snn_compiler/nn/modules.py:258-357 then snn_compiler/zoo/vgg.py:101-105).
     forward takes the reference's [T, B, C, H, W] (any memory format) and
-    returns bf16 spikes [T, B, C, Ho, Wo] in channels-last memory;
+    returns spikes [T, B, C, Ho, Wo] in channels-last memory, in ``out_dtype``
+    (default: the input's dtype; spikes are exact in every float dtype);
     ``forward_nhwc`` chains layers on contiguous NHWC bf16 [T, B, H, W, C].
     """
 
     def __init__(self, conv: nn.Conv2d, bn: nn.BatchNorm2d | None, *, pool: str | None = "max",
                  neuron: str = "lif", tau: float = 2.0, decay: float | None = None,
                  decay_input: bool = True, soft_reset: bool = False, v_threshold: float = 1.0,
-                 v_reset: float = 0.0):
+                 v_reset: float = 0.0, out_dtype: torch.dtype | None = None):
         super().__init__()
+        self.out_dtype = out_dtype
         if tuple(conv.kernel_size) != (3, 3) or tuple(conv.stride) != (1, 1) or \
                 tuple(conv.padding) != (1, 1) or tuple(conv.dilation) != (1, 1) or conv.groups != 1:
             raise ValueError("FusedConvBNLIFPool needs a 3x3 / stride 1 / padding 1 conv")
@@ -329,4 +331,5 @@ class FusedConvBNLIFPool(nn.Module):
                                    soft_reset=self.soft_reset, out=out, tile_hint=tile_hint)
 
     def forward(self, x_seq):
-        return self.forward_nhwc(to_nhwc_bf16(x_seq)).permute(0, 1, 4, 2, 3)
+        s = self.forward_nhwc(to_nhwc_bf16(x_seq)).permute(0, 1, 4, 2, 3)
+        return s.to(self.out_dtype or x_seq.dtype)

@@ -24,7 +24,10 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ..nn.modules import IFNode, LIFNode, FusedConvBNLIFPool
+from ..nn.modules import (
+    IFNode, LIFNode, FusedConvBNLIFPool, FusedConvBNNeuron, FusedConvNeuron, FusedLinearNeuron,
+)
+from ..passes.fuse import fuse_snn_model
 from ..kernels.conv import conv3x3_image_lif
 from ..kernels.fused import fold_conv_bn
 from ..kernels.linear import linear_bias_lif, linear_preact
@@ -84,11 +87,14 @@ class VGGSNN(nn.Module):
         self.neuron_kind = neuron
         self.neuron_kwargs = nk
 
+    # modules that take and return [T, B, ...] (snn_compiler/zoo/vgg.py:92-108)
+    _SEQ = (IFNode, LIFNode, FusedConvBNNeuron, FusedConvNeuron, FusedConvBNLIFPool)
+
     def forward(self, x_seq):
         T, B = x_seq.shape[0], x_seq.shape[1]
         x = x_seq
         for layer in self.features:
-            if isinstance(layer, (IFNode, LIFNode)):
+            if isinstance(layer, self._SEQ):
                 x = layer(x)
             else:
                 T_, B_ = x.shape[0], x.shape[1]
@@ -96,7 +102,7 @@ class VGGSNN(nn.Module):
                 x = y.view(T_, B_, *y.shape[1:])
         x = x.contiguous().reshape(T, B, -1)
         for layer in self.classifier:
-            if isinstance(layer, (IFNode, LIFNode)):
+            if isinstance(layer, (FusedLinearNeuron, IFNode, LIFNode)):
                 x = layer(x)
             else:
                 T_, B_ = x.shape[0], x.shape[1]
@@ -148,17 +154,24 @@ def vgg16_snn(**kw): return _build(VGG16_CFG, **kw)
 def vgg19_snn(**kw): return _build(VGG19_CFG, **kw)
 
 
-def _build(cfg, *, fused=False, init_bn=True, seed=None, gain=1.0, **kwargs):
-    """Reference _build (snn_compiler/zoo/vgg.py:134-143); ``seed`` selects the
-    deterministic seeded_init_, ``fused`` returns a FusedVGGSNN engine."""
+def _build(cfg, *, fused=False, engine=False, init_bn=True, seed=None, gain=1.0, **kwargs):
+    """Reference _build (snn_compiler/zoo/vgg.py:134-143).
+
+    ``fused=True`` runs :func:`snnk.passes.fuse_snn_model` on the model (as the
+    reference does; ``m._n_fused`` holds the count).  ``engine=True`` returns
+    the whole-network :class:`FusedVGGSNN` engine instead (max-pool variant,
+    static image input).  ``seed`` selects the deterministic seeded_init_."""
     m = VGGSNN(cfg, **kwargs)
     if seed is not None:
         seeded_init_(m, seed, gain)
     elif init_bn:
         _maybe_init_bn(m)
     m.eval()
-    if fused:
+    if engine:
         return FusedVGGSNN(m)
+    if fused:
+        m, n = fuse_snn_model(m, layout=kwargs.get("layout", "NCHW"))
+        m._n_fused = n
     return m
 
 
@@ -250,6 +263,10 @@ class FusedVGGSNN(nn.Module):
         with identical steps -> logits [T, B, num_classes] fp32."""
         if image.ndim == 5:
             assert image.shape[0] == self.T, f"expected T={self.T} steps"
+            # the engine computes the input layer once for a static image
+            if not all(torch.equal(image[0], image[t]) for t in range(1, image.shape[0])):
+                raise ValueError("FusedVGGSNN takes a static image (identical steps); run "
+                                 "vgg*_snn(fused=True) for time-varying input")
             image = image[0]
         image = image.float().contiguous()
         T, B = self.T, image.shape[0]
