@@ -34,6 +34,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # Packed-FP32 VALU forms are kept out of every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # No a*b+c contraction: the neuron updates round every product and sum
+    # to fp32 in the reference's order (explicit fmaf calls stay fused).
+    "-ffp-contract=off",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
