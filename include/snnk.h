@@ -42,6 +42,8 @@ extern "C" {
 #define SNNK_SPIKE_SAME  0   /* 0/1 in the input's element type            */
 #define SNNK_SPIKE_U8    1   /* 0/1 as uint8                                */
 #define SNNK_SPIKE_BF16  2   /* 0/1 as bf16 (input for the MFMA layers)      */
+#define SNNK_SPIKE_BITS  3   /* packed: bit k%32 of uint32 word k/32 of each step
+                                (NCL % 32 == 0); the layout snnk_binary_gemm reads */
 
 /* ---- threshold modes (snn_compiler/kernels/neurons.py:66-68) --------- */
 #define SNNK_THR_SCALAR      0
@@ -72,7 +74,8 @@ const char* snnk_status_string(int status);
  * vth      [C] (PER_CHANNEL) or [NCL] (PER_NEURON) float; unused if SCALAR
  * v_init   [NCL] float or NULL (state starts at 0)
  * v_out    [NCL] float or NULL: membrane state after the last step
- * spikes   [T, NCL] in spike_fmt, or NULL (only count_out wanted)
+ * spikes   [T, NCL] in spike_fmt, [T, NCL/32] uint32 words for SNNK_SPIKE_BITS,
+ *          or NULL (only count_out wanted)
  * count_out[NCL] float or NULL: sum over T of the spikes
  *
  * Per element and step t (all arithmetic fp32, rounded after every

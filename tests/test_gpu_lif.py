@@ -11,6 +11,8 @@ kernel rounds every operation as the oracle does).
 import itertools
 import zlib
 
+import numpy as np
+
 import pytest
 import torch
 
@@ -203,3 +205,43 @@ def test_bf16_spike_output_from_fp32():
         s = snnk.if_lif(src.to(DEV), neuron="lif", spike_dtype=torch.bfloat16)
         assert s.dtype == torch.bfloat16
         assert torch.equal(s.cpu().float(), on.naive_if_lif(src, neuron="lif").float())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("layout", ["NCHW", "NHWC"])
+def test_packed_spike_output(dtype, layout):
+    """if_lif_packed: the words are the oracle's spikes packed LSB-first along
+    the flat memory order (snn_compiler/kernels/attention.py:236-242 bit
+    order), for every input dtype, per-channel thresholds and NHWC memory."""
+    from oracle import bits as ob
+    T, B, C, H, W = 4, 2, 64, 3, 5
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(T, B, C, H, W, generator=g) * 1.5).to(dtype)
+    thr = (torch.rand(C, generator=g) + 0.5)
+    if layout == "NHWC":   # channels-last memory, NCHW labels
+        xd = x.permute(0, 1, 3, 4, 2).contiguous().to(DEV).permute(0, 1, 4, 2, 3)
+    else:
+        xd = x.to(DEV)
+    words = snnk.if_lif_packed(xd, neuron="lif", tau=3.0, v_threshold=thr.to(DEV), layout=layout)
+    ref, _, _ = on.lif_multistep(x.float(), neuron="lif", tau=3.0, v_threshold=thr)
+    flat = ref.permute(0, 1, 3, 4, 2) if layout == "NHWC" else ref
+    want = ob.pack_rows(flat.reshape(T, -1, 32).numpy()).reshape(T, -1)
+    assert np.array_equal(words.cpu().numpy().view(np.uint32), want)
+
+
+def test_packed_spikes_feed_binary_gemm():
+    """LIF -> packed words along K -> binary_gemm(a_packed=True) equals the
+    GEMM of the unpacked spikes (no separate pack pass)."""
+    T, R, K, N = 2, 64, 256, 96
+    g = torch.Generator().manual_seed(12)
+    x = (torch.randn(T, R, K, generator=g) * 1.5).to(DEV)
+    Wb = (torch.rand(K, N, generator=g) < 0.5).float().to(DEV)
+    words = snnk.if_lif_packed(x, neuron="lif", tau=2.0)
+    spikes = snnk.if_lif(x, neuron="lif", tau=2.0)
+    for signed in (False, True):
+        got = snnk.binary_gemm(words.view(T, R, K // 32), Wb.expand(T, K, N).contiguous(),
+                               a_packed=True, K=K, signed=signed)
+        want = snnk.binary_gemm(spikes, Wb.expand(T, K, N).contiguous(), signed=signed)
+        assert torch.equal(got, want)
+    with pytest.raises(ValueError):
+        snnk.if_lif_packed(torch.zeros(2, 3, 5, device=DEV))

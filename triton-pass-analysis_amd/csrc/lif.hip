@@ -131,13 +131,16 @@ __device__ __forceinline__ uint32_t channel_of(const LifArgs& a, uint64_t i) {
 }
 
 // Tag: input element type; SPK: 0 = spikes in the input type, 1 = uint8,
-// 2 = bf16;
+// 2 = bf16, 3 = packed bits (a lane's VEC spike bits are OR-combined across
+// the 32/VEC lanes of one 32-neuron word by xor shuffles; NCL % 32 == 0 makes
+// every word's lanes all active or all retired);
 // VEC: neurons per thread (VEC == 1 is the unaligned / ragged fallback).
 template <typename Tag, int SPK, int VEC, bool HAS_RES>
 __global__ __launch_bounds__(kBlock) void lif_kernel(LifArgs a) {
   typedef typename Tag::raw Raw;
   typedef typename std::conditional<
       SPK == 0, Raw, typename std::conditional<SPK == 1, uint8_t, uint16_t>::type>::type SRaw;
+  constexpr int kLanesPerWord = 32 / VEC;
   const uint64_t i0 =
       (static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x) * VEC;
   if (i0 >= static_cast<uint64_t>(a.NCL)) return;  // NCL % VEC == 0 when VEC > 1
@@ -175,6 +178,7 @@ __global__ __launch_bounds__(kBlock) void lif_kernel(LifArgs a) {
     for (int k = 0; k < kTChunk; ++k) {
       if (t0 + k < a.T) {
         Pack<SRaw, VEC> so;
+        uint32_t nib = 0;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
           float u = to_f32<Tag>(xs[k].v[j]);
@@ -186,9 +190,19 @@ __global__ __launch_bounds__(kBlock) void lif_kernel(LifArgs a) {
           cnt[j] += s ? 1.0f : 0.0f;
           if constexpr (SPK == 0) so.v[j] = spike_val<Tag>(s);
           else if constexpr (SPK == 1) so.v[j] = s ? 1 : 0;
-          else so.v[j] = s ? 0x3F80u : 0u;
+          else if constexpr (SPK == 2) so.v[j] = s ? 0x3F80u : 0u;
+          else nib |= (s ? 1u : 0u) << j;
         }
-        if (s_out) {
+        if constexpr (SPK == 3) {
+          const int lane = threadIdx.x & 63;
+          uint32_t w = nib << (VEC * (lane % kLanesPerWord));
+#pragma unroll
+          for (int m = 1; m < kLanesPerWord; m <<= 1) w |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), m));
+          if (s_out && lane % kLanesPerWord == 0) {
+            const uint64_t off = static_cast<uint64_t>(t0 + k) * (ncl / 32) + i0 / 32;
+            reinterpret_cast<uint32_t*>(a.spikes)[off] = w;
+          }
+        } else if (s_out) {
           const uint64_t off = static_cast<uint64_t>(t0 + k) * ncl + i0;
           store_pack<SRaw, VEC>(s_out + off, so);
         }
@@ -218,9 +232,10 @@ int dispatch_vec(const LifArgs& a, bool has_res, hipStream_t stream) {
   // The vector path needs every per-step row to start on a 16-byte boundary
   // of the input and spike buffers.
   constexpr int SBYTES = SPK == 0 ? sizeof(typename Tag::raw) : (SPK == 1 ? 1 : 2);
+  constexpr int SALIGN = SPK == 3 ? 4 : SBYTES * VEC;  // packed words: 4-byte stores
   bool vec_ok = (a.NCL % VEC == 0) && aligned(a.x, 16) &&
                 (!has_res || aligned(a.residual, 16)) &&
-                (a.spikes == nullptr || aligned(a.spikes, SBYTES * VEC)) &&
+                (a.spikes == nullptr || aligned(a.spikes, SALIGN)) &&
                 aligned(a.v_init, 16) && aligned(a.v_out, 16) &&
                 aligned(a.count_out, 16) &&
                 (a.thr_mode != SNNK_THR_PER_NEURON || aligned(a.vth, 16));
@@ -260,8 +275,11 @@ extern "C" int snnk_lif_forward(const void* x, int32_t x_dtype,
   if (spikes == nullptr && count_out == nullptr && v_out == nullptr) return SNNK_EINVAL;
   if (thr_mode < SNNK_THR_SCALAR || thr_mode > SNNK_THR_PER_NEURON) return SNNK_EINVAL;
   if (thr_mode != SNNK_THR_SCALAR && vth == nullptr) return SNNK_EINVAL;
-  if (spike_fmt != SNNK_SPIKE_SAME && spike_fmt != SNNK_SPIKE_U8 && spike_fmt != SNNK_SPIKE_BF16)
-    return SNNK_EINVAL;
+  if (spike_fmt < SNNK_SPIKE_SAME || spike_fmt > SNNK_SPIKE_BITS) return SNNK_EINVAL;
+  if (spike_fmt == SNNK_SPIKE_BITS) {
+    if (NCL % 32 != 0) return SNNK_EUNSUPPORTED;
+    if (!aligned(spikes, 4)) return SNNK_EALIGN;
+  }
   const bool need_c = bias != nullptr || thr_mode == SNNK_THR_PER_CHANNEL;
   if (need_c && (C <= 0 || HW <= 0)) return SNNK_EINVAL;
   if (C <= 0) C = 1;
@@ -288,14 +306,17 @@ extern "C" int snnk_lif_forward(const void* x, int32_t x_dtype,
     case SNNK_F32:
       return spike_fmt == SNNK_SPIKE_SAME ? dispatch_vec<F32, 0>(a, has_res, s)
              : spike_fmt == SNNK_SPIKE_U8 ? dispatch_vec<F32, 1>(a, has_res, s)
-                                          : dispatch_vec<F32, 2>(a, has_res, s);
+             : spike_fmt == SNNK_SPIKE_BF16 ? dispatch_vec<F32, 2>(a, has_res, s)
+                                            : dispatch_vec<F32, 3>(a, has_res, s);
     case SNNK_BF16:
       return spike_fmt == SNNK_SPIKE_U8 ? dispatch_vec<BF16, 1>(a, has_res, s)
-                                        : dispatch_vec<BF16, 0>(a, has_res, s);
+             : spike_fmt == SNNK_SPIKE_BITS ? dispatch_vec<BF16, 3>(a, has_res, s)
+                                            : dispatch_vec<BF16, 0>(a, has_res, s);
     case SNNK_F16:
       return spike_fmt == SNNK_SPIKE_SAME ? dispatch_vec<F16, 0>(a, has_res, s)
              : spike_fmt == SNNK_SPIKE_U8 ? dispatch_vec<F16, 1>(a, has_res, s)
-                                          : dispatch_vec<F16, 2>(a, has_res, s);
+             : spike_fmt == SNNK_SPIKE_BF16 ? dispatch_vec<F16, 2>(a, has_res, s)
+                                            : dispatch_vec<F16, 3>(a, has_res, s);
     default:
       return SNNK_EINVAL;
   }

@@ -21,7 +21,7 @@ OK, EINVAL, EUNSUPPORTED, EALIGN = 0, -1, -2, -3
 # element types
 F32, BF16, F16, U8, I32 = 0, 1, 2, 3, 4
 # spike formats
-SPIKE_SAME, SPIKE_U8, SPIKE_BF16 = 0, 1, 2
+SPIKE_SAME, SPIKE_U8, SPIKE_BF16, SPIKE_BITS = 0, 1, 2, 3
 # threshold modes
 THR_SCALAR, THR_PER_CHANNEL, THR_PER_NEURON = 0, 1, 2
 # binary GEMM algorithms

@@ -1,6 +1,6 @@
 """Operator entry points (mirror of snn_compiler/kernels/__init__.py:1-15, plus
 the fused conv / linear / attention operators of this library)."""
-from .neurons import if_lif
+from .neurons import if_lif, if_lif_packed
 from .binary import pack_bits, binary_gemm
 from .attention import (spike_ktv_popcount, spike_av_lif, spike_attention,
                         spike_self_attention, HAS_POPC)
@@ -12,7 +12,7 @@ from .fused import (
 )
 
 __all__ = [
-    "if_lif", "pack_bits", "binary_gemm",
+    "if_lif", "if_lif_packed", "pack_bits", "binary_gemm",
     "spike_ktv_popcount", "spike_av_lif", "spike_attention", "spike_self_attention", "HAS_POPC",
     "conv_bn_lif_pool", "conv3x3_bn_lif_nhwc", "conv3x3_image_lif", "to_nhwc_bf16",
     "linear_bias_lif", "linear_preact",

@@ -95,14 +95,16 @@ def launch_lif(x, *, bias=None, residual=None, thr=(THR_SCALAR, None, 1.0),
                v_init=None, v_out=None, spikes=None, count=None,
                C=1, HW=1, channel_last=False, decay=1.0, in_scale=1.0,
                v_reset=0.0, soft_reset=False):
-    """Enqueue snnk_lif_forward on the current stream of ``x``'s device."""
+    """Enqueue snnk_lif_forward on the current stream of ``x``'s device.
+    An int32 ``spikes`` tensor receives packed bits ([T, NCL/32] words)."""
     T = x.shape[0]
     NCL = x[0].numel() if T > 0 else 0
     thr_mode, thr_t, thr_s = thr
     sfmt = _abi.SPIKE_SAME
     if spikes is not None and spikes.dtype != x.dtype:
-        assert spikes.dtype in (torch.uint8, torch.bfloat16), spikes.dtype
-        sfmt = _abi.SPIKE_U8 if spikes.dtype == torch.uint8 else _abi.SPIKE_BF16
+        assert spikes.dtype in (torch.uint8, torch.bfloat16, torch.int32), spikes.dtype
+        sfmt = {torch.uint8: _abi.SPIKE_U8, torch.bfloat16: _abi.SPIKE_BF16,
+                torch.int32: _abi.SPIKE_BITS}[spikes.dtype]
     with torch.cuda.device(x.device):
         _abi.call(
             "snnk_lif_forward",
@@ -149,3 +151,42 @@ def if_lif(
                channel_last=(layout == "NHWC"), decay=df, in_scale=sc,
                v_reset=v_reset, soft_reset=soft_reset)
     return spike_seq
+
+
+def if_lif_packed(
+    x_seq: torch.Tensor,
+    *,
+    neuron: str = "if",
+    tau: float = 2.0,
+    decay: float | None = None,
+    decay_input: bool = True,
+    soft_reset: bool = False,
+    v_threshold=1.0,
+    v_reset: float = 0.0,
+    layout: str = "NCHW",
+) -> torch.Tensor:
+    """``if_lif`` writing bit-packed spikes: int32 words ``[T, NCL // 32]``.
+
+    Extension of snn_compiler/kernels/neurons.py:311-376.  Neuron ``i`` of a
+    step (flat memory order of ``x_seq[t]``) lands in bit ``i % 32`` of word
+    ``i // 32`` -- LSB first, the convention of ``pack_bits`` and the
+    reference's ``_pack_N``.  For channel-last activations (``[T, R, C]`` or
+    NHWC ``[T, B, C, H, W]`` with ``layout='NHWC'``) the words are packed along
+    C, so ``words.view(T, R, C // 32)`` is the ``a_packed`` operand of
+    :func:`snnk.binary_gemm`.  Needs ``NCL % 32 == 0``; 1/8 of the bytes of
+    uint8 spikes, 1/32 of fp32.
+    """
+    check_flat(x_seq, layout)
+    assert x_seq.dtype in (torch.float32, torch.float16, torch.bfloat16)
+    T = x_seq.shape[0]
+    NCL = x_seq[0].numel()
+    if NCL % 32 != 0:
+        raise ValueError(f"packed spikes need NCL % 32 == 0, got NCL={NCL}")
+    C, HW = infer_C_HW(x_seq)
+    df, sc = neuron_params(neuron, tau, decay, decay_input)
+    Cthr = x_seq.shape[2] if x_seq.ndim >= 4 else (x_seq.shape[-1] if x_seq.ndim == 3 else 1)
+    thr = resolve_threshold(v_threshold, Cthr, NCL)
+    words = torch.empty(T, NCL // 32, device=x_seq.device, dtype=torch.int32)
+    launch_lif(x_seq, thr=thr, spikes=words, C=C, HW=HW, channel_last=(layout == "NHWC"),
+               decay=df, in_scale=sc, v_reset=v_reset, soft_reset=soft_reset)
+    return words
