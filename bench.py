@@ -6,7 +6,8 @@
 Workloads: ``vgg16`` (config 4, the headline:
 VGG16-SNN T=4 B=32 images/s, with the B=1/56 curve and per-layer kernel
 rooflines), ``lif`` (config 0), ``bgemm`` (config 1), ``conv`` (config 2),
-``ssa`` (config 3).
+``ssa`` (config 3); ``copy`` (not in the default run) is a plain device
+copy that calibrates the HBM counters.
 A step is one pass of the hot path over one batch of synthetic, seeded input
 that is resident in HBM before timing starts.  Buffers rotate over several sets (> 512 MiB in total)
 so that the 256 MiB MALL cannot serve a step from the previous step's data.
@@ -42,6 +43,36 @@ import torch  # noqa: E402
 METRIC = "VGG16-SNN (T=4,B=32) images/sec; LIF HBM GB/s; binary GEMM TOPS vs peak"
 HBM_PEAK_GBS = 8000.0
 ROTATE_BYTES = 640 << 20
+
+
+TRAFFIC_TABLE = ROOT / "profiles" / "hbm_traffic.md"
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch of a workload's dominant kernel, from the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed in profiles/ (a table
+    row ``| workload | kernel | grid | fetch KiB | write KiB | bytes |``); None
+    when the table has no row for it."""
+    if not TRAFFIC_TABLE.exists():
+        return None
+    for line in TRAFFIC_TABLE.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 6 and cells[0] == workload:
+            try:
+                return {"bytes": float(cells[5]), "kernel": cells[1], "grid": cells[2],
+                        "fetch_kib": float(cells[3]), "write_kib": float(cells[4]),
+                        "source": "profiles/hbm_traffic.md"}
+            except ValueError:
+                return None
+    return None
+
+
+def _with_traffic(roof: dict, workload: str) -> dict:
+    t = measured_traffic(workload)
+    roof["traffic"] = None if t is None else t["bytes"]
+    if t is not None:
+        roof["traffic_detail"] = t
+    return roof
 
 
 def cpu_threads() -> int:
@@ -140,6 +171,20 @@ def bench_lif(args, dev):
     s_ref, v_ref, _ = on.lif_multistep(x_cpu, neuron="lif", tau=2.0)
     ok = torch.equal(ss[0].cpu(), s_ref) and torch.equal(vs[0].cpu(), v_ref)
 
+    # same step writing bit-packed spikes (x in, packed words out, final v)
+    from oracle import bits as ob
+    bits_bytes = T * NCL * 4 + T * NCL // 8 + NCL * 4
+    ws = [torch.empty(T, NCL // 32, device=dev, dtype=torch.int32) for _ in range(nsets)]
+
+    def step_bits(i):
+        launch_lif(xs[i], thr=(THR_SCALAR, None, 1.0), spikes=ws[i], v_out=vs[i],
+                   C=C, HW=H * W, decay=0.5, in_scale=0.5, v_reset=0.0)
+
+    wall_b, kern_b = time_gpu(step_bits, nsets, args.steps, args.warmup)
+    import numpy as np
+    want = ob.pack_rows(s_ref.reshape(T, -1, 32).numpy()).reshape(T, -1)
+    ok_bits = bool(np.array_equal(ws[0].cpu().numpy().view(np.uint32), want))
+
     rec = {
         "workload": "lif", "value": bytes_per / wall / 1e9, "unit": "GB/s",
         "ms_per_step": wall * 1e3, "dtype": "f32",
@@ -153,8 +198,15 @@ def bench_lif(args, dev):
                      "frac": bytes_per / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                      "traffic": None, "algorithmic_bytes": bytes_per,
                      "kernel_ms_mean": kern_ms},
-        "parity": ok,
+        "parity": ok and ok_bits,
+        "spikes_packed": {"value": bits_bytes / wall_b / 1e9, "unit": "GB/s",
+                          "algorithmic_bytes": bits_bytes, "kernel_ms_mean": kern_b,
+                          "frac": bits_bytes / (kern_b * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                          "parity": ok_bits},
     }
+    _with_traffic(rec["roofline"], "lif")
+    t = measured_traffic("lif_bits")
+    rec["spikes_packed"]["traffic"] = None if t is None else t["bytes"]
     if not args.no_cpu_baseline:
         nth = cpu_threads()
         torch.set_num_threads(nth)
@@ -231,6 +283,7 @@ def bench_bgemm(args, dev):
         "pack_A_ms": pack_ms,
         "parity": bool(ok),
     }
+    _with_traffic(rec["roofline"], "bgemm")
     if not args.no_cpu_baseline:
         torch.set_num_threads(cpu_threads())
         Af, Wf = A.float(), W.float()
@@ -309,6 +362,7 @@ def bench_conv(args, dev):
         "nchw_to_nhwc_ms": e0.elapsed_time(e1) / 20,
         "parity": agree >= 0.999,
     }
+    _with_traffic(rec["roofline"], "conv")
     if not args.no_cpu_baseline:
         torch.set_num_threads(cpu_threads())
         sec = time_cpu(lambda: of.conv_bn_lif_pool(x, w, None, gamma, beta, mean, var, 1e-5,
@@ -437,6 +491,7 @@ def bench_vgg(args, dev):
                          "parity": r["parity"]} for r in recs.values()],
         "parity": all(r["parity"] for r in recs.values()),
     }
+    _with_traffic(rec["roofline"], "vgg16/" + dom["layer"].split()[0])
     if not args.no_cpu_baseline:
         torch.set_num_threads(cpu_threads())
         img = recs[32]["img_cpu"]
@@ -517,6 +572,7 @@ def bench_ssa(args, dev):
         "qkv_spike_agreement_vs_fp32": qkv_agree,
         "parity": qkv_agree >= 0.999,
     }
+    _with_traffic(rec["roofline"], "ssa")
     if not args.no_cpu_baseline:
         torch.set_num_threads(cpu_threads())
         sec = time_cpu(lambda: oa.ssa_forward(x, p, heads=H, scale=0.125, vth_qkv=1.0,
@@ -529,8 +585,35 @@ def bench_ssa(args, dev):
     return rec
 
 
+# --------------------------------------------------------------------------
+# Plain device copy (calibration: practical HBM rate, and the known byte count
+# that scales the FETCH_SIZE / WRITE_SIZE counters)
+# --------------------------------------------------------------------------
+def bench_copy(args, dev):
+    nbytes = 64 << 20
+    nsets = max(2, math.ceil(ROTATE_BYTES / (2 * nbytes)))
+    src = [torch.rand(nbytes // 4, device=dev) for _ in range(nsets)]
+    dst = [torch.empty_like(src[0]) for _ in range(nsets)]
+
+    def step(i):
+        dst[i].copy_(src[i])
+
+    wall, kern_ms = time_gpu(step, nsets, args.steps, args.warmup)
+    ok = torch.equal(dst[0], src[0])
+    gbs = 2 * nbytes / (kern_ms * 1e-3) / 1e9
+    return {"workload": "copy", "value": 2 * nbytes / wall / 1e9, "unit": "GB/s",
+            "ms_per_step": wall * 1e3, "dtype": "f32",
+            "config": {"workload": "device_copy_64MiB", "bytes": nbytes, "rotating_sets": nsets},
+            "roofline": _with_traffic({"bound": "hbm", "kernel": "copy", "achieved": gbs,
+                                       "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                       "frac": gbs / HBM_PEAK_GBS,
+                                       "algorithmic_bytes": 2 * nbytes,
+                                       "kernel_ms_mean": kern_ms}, "copy"),
+            "parity": bool(ok)}
+
+
 WORKLOADS = {"vgg16": bench_vgg, "lif": bench_lif, "bgemm": bench_bgemm, "conv": bench_conv,
-             "ssa": bench_ssa}
+             "ssa": bench_ssa, "copy": bench_copy}
 HEADLINE_ORDER = ["vgg16", "lif", "bgemm", "conv", "ssa"]
 
 
