@@ -30,6 +30,7 @@ extern "C" {
 #define SNNK_EINVAL       -1   /* bad pointer / size / enum value          */
 #define SNNK_EUNSUPPORTED -2   /* valid request this build does not cover   */
 #define SNNK_EALIGN       -3   /* pointer alignment the kernel requires      */
+#define SNNK_EWORKSPACE   -4   /* workspace missing or smaller than needed   */
 
 /* ---- element types --------------------------------------------------- */
 #define SNNK_F32   0
@@ -185,6 +186,42 @@ int snnk_linear_bias_lif(const uint16_t* x, const uint16_t* w, const float* bias
                          int64_t R, int64_t K, int64_t N, float decay,
                          float in_scale, float v_threshold, float v_reset,
                          int32_t soft_reset, int32_t tile_hint, void* stream);
+
+/*
+ * Workspace variants of snnk_conv3x3_bn_lif and snnk_linear_bias_lif (same
+ * arguments and results; no reference counterpart: the reference path
+ * replaced is the same cuDNN conv / GEMM + fused LIF, fused.py:101-114).
+ * They may split K across `splits` workgroups per output tile (0 = chosen
+ * from the problem size, 1 = never): partial sums go to the caller's
+ * workspace and the last workgroup of each tile sums them in split order
+ * (deterministic) and runs the LIF epilogue.  The workspace starts with a
+ * fixed 256 KB region of per-tile ticket counters that must be zero before
+ * the first call (e.g. a zero-filled allocation); every call leaves it zero
+ * again, so one workspace serves any sequence of calls, of any shapes, on
+ * one stream -- calls that run concurrently must not share it.  16-byte x/w and 256-byte workspace
+ * alignment.  *_ws_size returns the bytes needed for the same shape and
+ * hints (0 when no split is chosen) or a negative status; a call with a
+ * smaller workspace returns SNNK_EWORKSPACE.
+ */
+int snnk_conv3x3_bn_lif_ws(const uint16_t* x, const uint16_t* w, const float* bias,
+                           uint16_t* spikes_out, float* preact_out,
+                           int64_t T, int64_t B, int64_t H, int64_t W,
+                           int64_t Cin, int64_t Cout, int32_t pool,
+                           float decay, float in_scale, float v_threshold,
+                           float v_reset, int32_t soft_reset, int32_t tile_hint,
+                           int32_t splits, void* workspace, int64_t workspace_bytes,
+                           void* stream);
+int64_t snnk_conv3x3_bn_lif_ws_size(int64_t T, int64_t B, int64_t H, int64_t W,
+                                    int64_t Cin, int64_t Cout, int32_t pool, int32_t preact,
+                                    int32_t tile_hint, int32_t splits);
+int snnk_linear_bias_lif_ws(const uint16_t* x, const uint16_t* w, const float* bias,
+                            uint16_t* spikes_out, float* preact_out, int64_t T,
+                            int64_t R, int64_t K, int64_t N, float decay,
+                            float in_scale, float v_threshold, float v_reset,
+                            int32_t soft_reset, int32_t tile_hint, int32_t splits,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+int64_t snnk_linear_bias_lif_ws_size(int64_t T, int64_t R, int64_t K, int64_t N,
+                                     int32_t preact, int32_t tile_hint, int32_t splits);
 
 /*
  * Spike self-attention core: per (batch, head) and step t, integer

@@ -45,3 +45,23 @@ def test_invalid_arguments_rejected_without_gpu():
                               ctypes.c_void_p(16), 0, None, 4, 10, 1, 1, 0, 0.5, 0.5, 0.0,
                               0, None)
     assert st == _abi.EINVAL
+
+
+def test_workspace_size_queries_without_gpu():
+    """The split-K workspace size is pure host arithmetic: no split (1) needs
+    none, a deep small-M layer gets a split and a ticket array + partials."""
+    from snnk import _abi
+    for name in _abi.SIZE_PROTOTYPES:
+        assert name in declared_symbols(), name
+    size = lambda *a: _abi.lib().snnk_conv3x3_bn_lif_ws_size(*a)  # noqa: E731
+    # T, B, H, W, Cin, Cout, pool, preact, tile_hint, splits
+    assert size(4, 32, 4, 4, 512, 512, 0, 0, -1, 1) == 0
+    n = size(4, 32, 4, 4, 512, 512, 0, 0, 2, 4)          # 128x128 tiles, 4 splits
+    tiles = (2048 // 128) * (512 // 128)
+    assert n == 65536 * 4 + tiles * 4 * 128 * 128 * 4    # fixed ticket region + partials
+    assert size(4, 32, 4, 4, 512, 512, 0, 0, -1, 0) > 0  # auto split for a deep layer
+    assert size(4, 32, 4, 4, 500, 512, 0, 0, -1, 0) == _abi.EUNSUPPORTED
+    assert size(4, 32, 4, 4, 512, 512, 1, 1, -1, 0) == _abi.EINVAL   # preact + pool
+    lin = _abi.lib().snnk_linear_bias_lif_ws_size
+    assert lin(4, 32, 4096, 4096, 0, -1, 1) == 0 and lin(4, 32, 4096, 4096, 0, -1, 0) > 0
+    assert _abi.lib().snnk_status_string(_abi.EWORKSPACE) == b"workspace missing or too small"

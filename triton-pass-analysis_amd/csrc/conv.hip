@@ -29,6 +29,8 @@
 // tile (group g: stages g, g+KS, ...; a group past the last stage loads
 // zeros) and are summed through LDS before the epilogue (split-K for the
 // small late layers).  Operand stages are double buffered in LDS.
+#include <algorithm>
+
 #include "snnk_common.h"
 
 namespace snnk {
@@ -79,6 +81,12 @@ struct ConvArgs {
   uint32_t w_bytes;      // bytes of w, below kOOB
   int64_t o_tstride;     // B*Ho*Wo*Cout
   int tiles_m, tiles_n;  // output tiles along rows (quads) and Cout
+  // cross-block split-K: `splits` blocks share one output tile, each over
+  // `stages_per_split` K stages; partial sums go to `partials`, the last
+  // block of a tile (ticket in `tickets`) reduces them in split order
+  int splits, stages_per_split;
+  float* partials;
+  unsigned int* tickets;
   float decay, in_scale, vth, v_reset;
   int soft_reset;
 };
@@ -130,15 +138,32 @@ void conv3x3_kernel(ConvArgs a) {
   const int wmn = wave - kg * (WM * WN);
   const int wm = wmn / WN, wn = wmn - wm * WN;
   // Workgroups are dealt to the 8 XCDs round-robin by id; id -> tile is
-  // remapped so that each XCD runs one contiguous range of tiles (row tile
-  // major, Cout tile minor) and its L2 holds only that range's activations.
-  const int n_tiles = a.tiles_m * a.tiles_n;
+  // remapped so that each XCD runs one contiguous range of tiles.  Without
+  // split-K the range is row-tile major (an XCD's L2 holds its rows'
+  // activations); with split-K it is (split, Cout tile) major, so each XCD
+  // streams its own slice of the weights once.
+  const int n_mn = a.tiles_m * a.tiles_n;
+  const int n_tiles = n_mn * a.splits;
   const int per_xcd = (n_tiles + 7) / 8;
   const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (tile >= n_tiles) return;  // whole workgroup: no barrier is left waiting
-  const int tm = tile / a.tiles_n;
+  int tm, tn, split;
+  if (a.splits == 1) {
+    tm = tile / a.tiles_n;
+    tn = tile - tm * a.tiles_n;
+    split = 0;
+  } else {
+    tm = tile % a.tiles_m;
+    const int rest = tile / a.tiles_m;
+    tn = rest % a.tiles_n;
+    split = rest / a.tiles_n;
+  }
+  const int mn = tm * a.tiles_n + tn;  // output tile id
   const int quad0 = tm * C::kQuads;
-  const int n0 = (tile - tm * a.tiles_n) * C::BN;
+  const int n0 = tn * C::BN;
+  // this block's K stages [st_begin, st_end)
+  const int st_begin = split * a.stages_per_split;
+  const int st_end = min(a.n_stages, st_begin + a.stages_per_split);
   const int HW = a.H * a.W;
   const int K = TAPS * a.Cin;
 
@@ -205,7 +230,7 @@ void conv3x3_kernel(ConvArgs a) {
     }
   }
 
-  const int n_stages_g = (a.n_stages + KSPLIT - 1) / KSPLIT;
+  const int n_stages_g = (st_end - st_begin + KSPLIT - 1) / KSPLIT;
   const int n_chunks = (a.T + 3) / 4;
 
   // membrane state of the epilogue waves: [TM][TN][4 pixels]
@@ -226,6 +251,58 @@ void conv3x3_kernel(ConvArgs a) {
     col_ok[j] = n < a.Cout;
     bias_n[j] = (a.bias && col_ok[j]) ? a.bias[n] : 0.0f;
   }
+
+  // bias + LIF over the 4 steps of chunk tc (+ 2x2 OR), or the fp32
+  // pre-activations; run by the kg == 0 waves on the full K sum
+  auto epilogue = [&](const f32x16 (&acc)[TM][TN], int tc) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int quad = quad0 + (wm * TM + i) * 2 + g_lane;
+      if (quad >= a.n_quads) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if (!col_ok[j]) continue;
+        const int n = n0 + (wn * TN + j) * 32 + r_lane;
+        if constexpr (MODE == MODE_PREACT) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const int tg = tc * 4 + t;
+              if (tg < a.T) {
+                const int64_t p = static_cast<int64_t>(quad) * 4 + q;
+                a.pre[tg * a.o_tstride + p * a.Cout + n] = __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]);
+              }
+            }
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int tg = tc * 4 + t;
+            if (tg >= a.T) break;
+            bool any = false;
+            bool sp[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float u = __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]);
+              const float h = __fadd_rn(__fmul_rn(a.decay, v[i][j][q]), __fmul_rn(a.in_scale, u));
+              const bool s = h >= a.vth;
+              v[i][j][q] = s ? (a.soft_reset ? __fsub_rn(h, a.vth) : a.v_reset) : h;
+              sp[q] = s;
+              any = any || s;
+            }
+            uint16_t* o = a.out + static_cast<int64_t>(tg) * a.o_tstride;
+            if constexpr (POOL) {
+              o[static_cast<int64_t>(quad) * a.Cout + n] = spike_bf16(any);
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                o[(static_cast<int64_t>(quad) * 4 + q) * a.Cout + n] = spike_bf16(sp[q]);
+            }
+          }
+        }
+      }
+    }
+  };
 
   for (int tc = 0; tc < n_chunks; ++tc) {
     f32x16 acc[TM][TN];
@@ -253,8 +330,8 @@ void conv3x3_kernel(ConvArgs a) {
     };
     auto stage_addr = [&](int sl) {
       StageAddr p;
-      const int sg = sl * KSPLIT + kg;
-      p.live = sg < a.n_stages;
+      const int sg = st_begin + sl * KSPLIT + kg;
+      p.live = sg < st_end;
       const int k0 = p.live ? sg * kKS : 0;
       // tap and channel offset of each 32-wide half of the stage; a half at
       // or past K gets tap TAPS, which no source pixel mask contains
@@ -372,94 +449,179 @@ void conv3x3_kernel(ConvArgs a) {
       __syncthreads();
     }
 
-    // ---- epilogue: bias + LIF over the 4 steps (+ 2x2 OR) -------------------
     if (kg == 0) {
+      if (a.splits == 1) {
+        epilogue(acc, tc);
+      } else {
+        float* dst = a.partials + ((static_cast<int64_t>(mn) * a.splits + split) * n_chunks + tc) *
+                                      (C::BM * C::BN) + wmn * (TM * TN * 16 * 64) + lane;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int quad = quad0 + (wm * TM + i) * 2 + g_lane;
-        if (quad >= a.n_quads) continue;
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          if (!col_ok[j]) continue;
-          const int n = n0 + (wn * TN + j) * 32 + r_lane;
-          if constexpr (MODE == MODE_PREACT) {
+          for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-              for (int t = 0; t < 4; ++t) {
-                const int tg = tc * 4 + t;
-                if (tg < a.T) {
-                  const int64_t p = static_cast<int64_t>(quad) * 4 + q;
-                  a.pre[tg * a.o_tstride + p * a.Cout + n] = __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]);
-                }
-              }
-          } else {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const int tg = tc * 4 + t;
-              if (tg >= a.T) break;
-              bool any = false;
-              bool sp[4];
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const float u = __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]);
-                const float h = __fadd_rn(__fmul_rn(a.decay, v[i][j][q]), __fmul_rn(a.in_scale, u));
-                const bool s = h >= a.vth;
-                v[i][j][q] = s ? (a.soft_reset ? __fsub_rn(h, a.vth) : a.v_reset) : h;
-                sp[q] = s;
-                any = any || s;
-              }
-              uint16_t* o = a.out + static_cast<int64_t>(tg) * a.o_tstride;
-              if constexpr (POOL) {
-                o[static_cast<int64_t>(quad) * a.Cout + n] = spike_bf16(any);
-              } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                  o[(static_cast<int64_t>(quad) * 4 + q) * a.Cout + n] = spike_bf16(sp[q]);
-              }
-            }
-          }
-        }
+            for (int e = 0; e < 16; ++e)
+              // system-coherent store: written through to memory, past this XCD's L2
+              __hip_atomic_store(dst + ((i * TN + j) * 16 + e) * 64, acc[i][j][e],
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
     }
+  }
+
+  // ---- cross-block split-K: the last block of a tile reduces and fires -----
+  if (a.splits > 1) {
+    // The partials were stored write-through and are read back with
+    // system-coherent loads, so no cache-wide fence is needed (an agent-scope
+    // fence writes back and invalidates the whole L2 of the XCD): each wave
+    // waits for its stores to be acknowledged, then one ticket per block.
+    // The operand ring is idle now; its first word carries the ticket result.
+    volatile unsigned int* s_last = reinterpret_cast<volatile unsigned int*>(smem);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+      *s_last = __hip_atomic_fetch_add(a.tickets + mn, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) ==
+                static_cast<unsigned int>(a.splits - 1);
+    __syncthreads();
+    if (!*s_last) return;
+    if (kg == 0) {
+      for (int tc = 0; tc < n_chunks; ++tc) {
+        f32x16 acc[TM][TN];
+        const float* src = a.partials + static_cast<int64_t>(mn) * a.splits * n_chunks * (C::BM * C::BN) +
+                           static_cast<int64_t>(tc) * (C::BM * C::BN) + wmn * (TM * TN * 16 * 64) + lane;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              acc[i][j][e] = __hip_atomic_load(src + ((i * TN + j) * 16 + e) * 64, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_SYSTEM);
+        for (int sp = 1; sp < a.splits; ++sp) {  // fixed summation order
+          const float* p = src + static_cast<int64_t>(sp) * n_chunks * (C::BM * C::BN);
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+              for (int e = 0; e < 16; ++e)
+                acc[i][j][e] += __hip_atomic_load(p + ((i * TN + j) * 16 + e) * 64, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        epilogue(acc, tc);
+      }
+    }
+    if (tid == 0)  // ready for the next launch
+      __hip_atomic_store(a.tickets + mn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int MODE, int TAPS>
 int launch_cfg(const ConvArgs& a, hipStream_t stream) {
   using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF>;
-  ConvArgs b = a;
-  b.tiles_m = (a.n_quads + C::kQuads - 1) / C::kQuads;
-  b.tiles_n = (a.Cout + C::BN - 1) / C::BN;
-  const int64_t per_xcd = (static_cast<int64_t>(b.tiles_m) * b.tiles_n + 7) / 8;
+  const int64_t per_xcd = (static_cast<int64_t>(a.tiles_m) * a.tiles_n * a.splits + 7) / 8;
   if (per_xcd * 8 > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
   hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, NBUF, POOL, MODE, TAPS>),
-                     dim3(static_cast<unsigned>(per_xcd * 8)), dim3(C::kThreads), 0, stream, b);
+                     dim3(static_cast<unsigned>(per_xcd * 8)), dim3(C::kThreads), 0, stream, a);
   return launch_status();
 }
 
 constexpr int kNumTiles = 19;
+struct TileShape { int bm, bn; };
+//                                   0          1         2          3         4        5
+constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 128}, {32, 32}, {32, 128},
+//   6         7         8          9           10         11          12         13
+    {32, 32}, {32, 64}, {32, 128}, {128, 128}, {128, 64}, {128, 128}, {128, 64}, {32, 64},
+//   14          15          16         17         18
+    {256, 128}, {128, 128}, {64, 128}, {128, 64}, {32, 128}};
 
 // Tile shape by problem size (rows = output rows of one 4-step chunk, K =
 // 9*Cin or the Linear depth): big tiles while M fills 256 CUs, split-K wave
 // groups as M shrinks and K grows.
-template <bool POOL, int MODE, int TAPS>
-int dispatch(const ConvArgs& a, int tile_hint, hipStream_t s) {
-  const int64_t rows = static_cast<int64_t>(a.n_quads) * 16;  // per T-chunk
+int auto_cfg(const ConvArgs& a) {
+  const int64_t rows = static_cast<int64_t>(a.n_quads) * 16;
   const int64_t K = static_cast<int64_t>(a.n_stages) * kKS;
-  int cfg = tile_hint;
-  if (cfg < 0) {
-    if (rows >= 65536) cfg = 1;                                        // 256 x 64
-    else if (rows >= 32768) cfg = a.Cout >= 256 ? 14 : (K <= 576 ? 3 : 9);
-    else if (rows >= 8192) cfg = 3;                                    // 64 x 128
-    else if (rows >= 2048) cfg = 8;                                    // 32 x 128 split-K 4
-    else if (rows >= 512) cfg = 4;                                     // 32 x 32 split-K 4
-    else if (a.Cout <= 64) cfg = 6;                                    // 32 x 32 split-K 8
-    else if (K <= 1024) cfg = 7;                                       // 32 x 64 split-K 4
-    else cfg = rows >= 128 ? 13 : 4;
+  if (rows >= 65536) return 1;                                        // 256 x 64
+  if (rows >= 32768) return a.Cout >= 256 ? 14 : (K <= 576 ? 3 : 9);
+  if (rows >= 8192) return 3;                                         // 64 x 128
+  if (rows >= 2048) return 8;                                         // 32 x 128 split-K 4
+  if (rows >= 512) return 4;                                          // 32 x 32 split-K 4
+  if (a.Cout <= 64) return 6;                                         // 32 x 32 split-K 8
+  if (K <= 1024) return 7;                                            // 32 x 64 split-K 4
+  return rows >= 128 ? 13 : 4;
+}
+
+// Tile shape and cross-block split when a workspace can be used, from a
+// sweep of both over the VGG16 / SSA shapes: splitting pays for the
+// weight-streaming small-M layers (FC, 4x4 with K = 4608).
+void auto_cfg_split(const ConvArgs& a, int* cfg, int* splits) {
+  const int64_t rows = static_cast<int64_t>(a.n_quads) * 16;
+  const int64_t K = static_cast<int64_t>(a.n_stages) * kKS;
+  *cfg = auto_cfg(a);
+  *splits = 1;
+  if (rows > 2048 || rows < 16) return;
+  if (rows > 512) {
+    if (K >= 4096) { *cfg = 3; *splits = 4; }                         // 64 x 128, 4 splits
+  } else if (rows <= 128) {
+    if (a.Cout <= 64) { *cfg = 4; *splits = 4; }                      // 32 x 32
+    else if (K > 1024) { *cfg = 13; *splits = 2; }                    // 32 x 64
   }
+}
+
+// Workspace layout: a fixed ticket region (one counter per output tile,
+// always at the same place so counters stay zero across calls of any shape)
+// followed by the partial sums of the current call.
+constexpr int64_t kMaxTickets = 65536;
+constexpr int64_t kTicketBytes = kMaxTickets * 4;
+
+struct Plan {
+  int cfg, splits, stages_per_split, tiles_m, tiles_n;
+  int64_t ticket_bytes, ws_bytes;
+};
+
+int make_plan(const ConvArgs& a, int tile_hint, int splits_hint, bool allow_split, Plan* p) {
+  if (tile_hint >= kNumTiles || splits_hint < 0) return SNNK_EINVAL;
+  int auto_splits = 1;
+  if (tile_hint >= 0) p->cfg = tile_hint;
+  else if (allow_split && splits_hint != 1) auto_cfg_split(a, &p->cfg, &auto_splits);
+  else p->cfg = auto_cfg(a);
+  const TileShape ts = kTile[p->cfg];
+  p->tiles_m = (a.n_quads + ts.bm / 16 - 1) / (ts.bm / 16);
+  p->tiles_n = (a.Cout + ts.bn - 1) / ts.bn;
+  const int64_t mn = static_cast<int64_t>(p->tiles_m) * p->tiles_n;
+  int splits = 1;
+  if (allow_split) {
+    if (splits_hint > 0) splits = splits_hint;
+    else if (tile_hint < 0) splits = auto_splits;
+    else if (mn < 160) splits = static_cast<int>((256 + mn - 1) / mn);  // fill the GPU
+    // at least 4 K stages per split; tile ids must fit the ticket region
+    splits = std::max(1, std::min(splits, a.n_stages / 4));
+    if (mn > kMaxTickets) splits = 1;
+  }
+  p->stages_per_split = (a.n_stages + splits - 1) / splits;
+  p->splits = (a.n_stages + p->stages_per_split - 1) / p->stages_per_split;  // none empty
+  p->ticket_bytes = 0;
+  p->ws_bytes = 0;
+  if (p->splits > 1) {
+    const int64_t n_chunks = (a.T + 3) / 4;
+    p->ticket_bytes = kTicketBytes;
+    p->ws_bytes = p->ticket_bytes + mn * p->splits * n_chunks * ts.bm * ts.bn * 4;
+  }
+  return SNNK_OK;
+}
+
+template <bool POOL, int MODE, int TAPS>
+int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) {
+  ConvArgs a = a0;
+  a.tiles_m = p.tiles_m;
+  a.tiles_n = p.tiles_n;
+  a.splits = p.splits;
+  a.stages_per_split = p.stages_per_split;
+  a.tickets = static_cast<unsigned int*>(workspace);
+  a.partials = p.splits > 1
+      ? reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + p.ticket_bytes) : nullptr;
   //                               WM WN TM TN KS NBUF           block tile, LDS
-  switch (cfg) {
+  switch (p.cfg) {
     case 0: return launch_cfg<2, 2, 2, 4, 1, 3, POOL, MODE, TAPS>(a, s);   // 128 x 256, 144 KB
     case 1: return launch_cfg<4, 1, 2, 2, 1, 2, POOL, MODE, TAPS>(a, s);   // 256 x 64, 80 KB
     case 2: return launch_cfg<2, 2, 2, 2, 1, 2, POOL, MODE, TAPS>(a, s);   // 128 x 128, 64 KB
@@ -483,26 +645,19 @@ int dispatch(const ConvArgs& a, int tile_hint, hipStream_t s) {
   }
 }
 
-}  // namespace
-}  // namespace snnk
-
-using namespace snnk;
-
-extern "C" int snnk_conv3x3_bn_lif(const uint16_t* x, const uint16_t* w, const float* bias,
-                                   uint16_t* spikes_out, float* preact_out,
-                                   int64_t T, int64_t B, int64_t H, int64_t W,
-                                   int64_t Cin, int64_t Cout, int32_t pool,
-                                   float decay, float in_scale, float v_threshold,
-                                   float v_reset, int32_t soft_reset, int32_t tile_hint,
-                                   void* stream) {
+// Validates a conv call and fills ConvArgs (no launch).
+int conv_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_t* spikes_out,
+              float* preact_out, int64_t T, int64_t B, int64_t H, int64_t W, int64_t Cin,
+              int64_t Cout, int32_t pool, float decay, float in_scale, float v_threshold,
+              float v_reset, int32_t soft_reset, bool check_ptrs, ConvArgs* out) {
   if (T < 0 || B < 0 || H < 0 || W < 0 || Cin <= 0 || Cout <= 0) return SNNK_EINVAL;
-  if (T == 0 || B == 0 || H == 0 || W == 0) return SNNK_OK;
-  if (x == nullptr || w == nullptr) return SNNK_EINVAL;
   const bool preact = preact_out != nullptr;
-  if (!preact && spikes_out == nullptr) return SNNK_EINVAL;
+  if (check_ptrs) {
+    if (x == nullptr || w == nullptr) return SNNK_EINVAL;
+    if (!preact && spikes_out == nullptr) return SNNK_EINVAL;
+  }
   if (preact && pool) return SNNK_EINVAL;
   if (Cin % 32 != 0 || Cout % 32 != 0) return SNNK_EUNSUPPORTED;
-  if (tile_hint >= kNumTiles) return SNNK_EINVAL;
   if (pool && (H % 2 != 0 || W % 2 != 0)) return SNNK_EUNSUPPORTED;
   if (!pool && (B * H * W) % 4 != 0) return SNNK_EUNSUPPORTED;
   const int64_t step_in = B * H * W * Cin;
@@ -510,8 +665,7 @@ extern "C" int snnk_conv3x3_bn_lif(const uint16_t* x, const uint16_t* w, const f
   // byte offsets into x and w are 32-bit (buffer descriptors)
   if (T * step_in * 2 > kOOB || T * step_out > (1ll << 40) || Cout * 9 * Cin * 2 > kOOB)
     return SNNK_EUNSUPPORTED;
-  if (!aligned(x, 16) || !aligned(w, 16)) return SNNK_EALIGN;
-
+  if (check_ptrs && (!aligned(x, 16) || !aligned(w, 16))) return SNNK_EALIGN;
   ConvArgs a{};
   a.x = x; a.w = w; a.bias = bias; a.out = spikes_out; a.pre = preact_out;
   a.T = static_cast<int>(T); a.B = static_cast<int>(B);
@@ -528,29 +682,24 @@ extern "C" int snnk_conv3x3_bn_lif(const uint16_t* x, const uint16_t* w, const f
   a.o_tstride = B * a.Ho * a.Wo * Cout;
   a.decay = decay; a.in_scale = in_scale; a.vth = v_threshold; a.v_reset = v_reset;
   a.soft_reset = soft_reset ? 1 : 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (preact) return dispatch<false, MODE_PREACT, 9>(a, tile_hint, s);
-  if (pool) return dispatch<true, MODE_LIF, 9>(a, tile_hint, s);
-  return dispatch<false, MODE_LIF, 9>(a, tile_hint, s);
+  *out = a;
+  return SNNK_OK;
 }
 
-// Linear + bias + LIF over T: x [T][R][K] bf16 rows, w [N][K] bf16 (the
-// nn.Linear weight layout), one 1x1-conv pass of the same kernel.
-extern "C" int snnk_linear_bias_lif(const uint16_t* x, const uint16_t* w, const float* bias,
-                                    uint16_t* spikes_out, float* preact_out, int64_t T,
-                                    int64_t R, int64_t K, int64_t N, float decay,
-                                    float in_scale, float v_threshold, float v_reset,
-                                    int32_t soft_reset, int32_t tile_hint, void* stream) {
+// Linear over the rows of [T][R][K]: the 1x1 case of the same kernel.
+int linear_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_t* spikes_out,
+                float* preact_out, int64_t T, int64_t R, int64_t K, int64_t N, float decay,
+                float in_scale, float v_threshold, float v_reset, int32_t soft_reset,
+                bool check_ptrs, ConvArgs* out) {
   if (T < 0 || R < 0 || K <= 0 || N <= 0) return SNNK_EINVAL;
-  if (T == 0 || R == 0) return SNNK_OK;
-  if (x == nullptr || w == nullptr) return SNNK_EINVAL;
-  const bool preact = preact_out != nullptr;
-  if (!preact && spikes_out == nullptr) return SNNK_EINVAL;
+  if (check_ptrs) {
+    if (x == nullptr || w == nullptr) return SNNK_EINVAL;
+    if (preact_out == nullptr && spikes_out == nullptr) return SNNK_EINVAL;
+  }
   if (K % 32 != 0 || N % 32 != 0 || R % 4 != 0) return SNNK_EUNSUPPORTED;
-  if (tile_hint >= kNumTiles) return SNNK_EINVAL;
   if (T * R * K * 2 > kOOB || N * K * 2 > kOOB || T * R * N > (1ll << 40))
     return SNNK_EUNSUPPORTED;
-  if (!aligned(x, 16) || !aligned(w, 16)) return SNNK_EALIGN;
+  if (check_ptrs && (!aligned(x, 16) || !aligned(w, 16))) return SNNK_EALIGN;
   ConvArgs a{};
   a.x = x; a.w = w; a.bias = bias; a.out = spikes_out; a.pre = preact_out;
   a.T = static_cast<int>(T); a.B = 1; a.H = 1; a.W = static_cast<int>(R);
@@ -565,7 +714,114 @@ extern "C" int snnk_linear_bias_lif(const uint16_t* x, const uint16_t* w, const 
   a.o_tstride = R * N;
   a.decay = decay; a.in_scale = in_scale; a.vth = v_threshold; a.v_reset = v_reset;
   a.soft_reset = soft_reset ? 1 : 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (preact) return dispatch<false, MODE_PREACT, 1>(a, tile_hint, s);
-  return dispatch<false, MODE_LIF, 1>(a, tile_hint, s);
+  *out = a;
+  return SNNK_OK;
+}
+
+template <int TAPS>
+int run(const ConvArgs& a, bool pool, int tile_hint, int splits, bool allow_split, void* ws,
+        int64_t ws_bytes, hipStream_t s) {
+  if (a.T == 0 || a.n_quads == 0) return SNNK_OK;
+  Plan p;
+  int st = make_plan(a, tile_hint, splits, allow_split, &p);
+  if (st != SNNK_OK) return st;
+  if (p.ws_bytes > 0 && (ws == nullptr || ws_bytes < p.ws_bytes)) return SNNK_EWORKSPACE;
+  if (p.ws_bytes > 0 && !aligned(ws, 256)) return SNNK_EALIGN;
+  if (a.pre != nullptr) return dispatch<false, MODE_PREACT, TAPS>(a, p, ws, s);
+  if (pool) return dispatch<true, MODE_LIF, TAPS>(a, p, ws, s);
+  return dispatch<false, MODE_LIF, TAPS>(a, p, ws, s);
+}
+
+}  // namespace
+}  // namespace snnk
+
+using namespace snnk;
+
+extern "C" int snnk_conv3x3_bn_lif(const uint16_t* x, const uint16_t* w, const float* bias,
+                                   uint16_t* spikes_out, float* preact_out,
+                                   int64_t T, int64_t B, int64_t H, int64_t W,
+                                   int64_t Cin, int64_t Cout, int32_t pool,
+                                   float decay, float in_scale, float v_threshold,
+                                   float v_reset, int32_t soft_reset, int32_t tile_hint,
+                                   void* stream) {
+  ConvArgs a;
+  if (T == 0 || B == 0 || H == 0 || W == 0) return (T < 0 || B < 0 || H < 0 || W < 0) ? SNNK_EINVAL : SNNK_OK;
+  int st = conv_args(x, w, bias, spikes_out, preact_out, T, B, H, W, Cin, Cout, pool, decay,
+                     in_scale, v_threshold, v_reset, soft_reset, true, &a);
+  if (st != SNNK_OK) return st;
+  return run<9>(a, pool != 0, tile_hint, 1, false, nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int snnk_conv3x3_bn_lif_ws(const uint16_t* x, const uint16_t* w, const float* bias,
+                                      uint16_t* spikes_out, float* preact_out,
+                                      int64_t T, int64_t B, int64_t H, int64_t W,
+                                      int64_t Cin, int64_t Cout, int32_t pool,
+                                      float decay, float in_scale, float v_threshold,
+                                      float v_reset, int32_t soft_reset, int32_t tile_hint,
+                                      int32_t splits, void* workspace, int64_t workspace_bytes,
+                                      void* stream) {
+  ConvArgs a;
+  if (T == 0 || B == 0 || H == 0 || W == 0) return (T < 0 || B < 0 || H < 0 || W < 0) ? SNNK_EINVAL : SNNK_OK;
+  int st = conv_args(x, w, bias, spikes_out, preact_out, T, B, H, W, Cin, Cout, pool, decay,
+                     in_scale, v_threshold, v_reset, soft_reset, true, &a);
+  if (st != SNNK_OK) return st;
+  return run<9>(a, pool != 0, tile_hint, splits, true, workspace, workspace_bytes,
+                static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t snnk_conv3x3_bn_lif_ws_size(int64_t T, int64_t B, int64_t H, int64_t W,
+                                               int64_t Cin, int64_t Cout, int32_t pool,
+                                               int32_t preact, int32_t tile_hint,
+                                               int32_t splits) {
+  if (T == 0 || B == 0 || H == 0 || W == 0) return (T < 0 || B < 0 || H < 0 || W < 0) ? SNNK_EINVAL : 0;
+  ConvArgs a;
+  float dummy = 0.0f;
+  int st = conv_args(nullptr, nullptr, nullptr, nullptr, preact ? &dummy : nullptr, T, B, H, W,
+                     Cin, Cout, pool, 0.f, 0.f, 0.f, 0.f, 0, false, &a);
+  if (st != SNNK_OK) return st;
+  Plan p;
+  st = make_plan(a, tile_hint, splits, true, &p);
+  return st != SNNK_OK ? st : p.ws_bytes;
+}
+
+extern "C" int snnk_linear_bias_lif(const uint16_t* x, const uint16_t* w, const float* bias,
+                                    uint16_t* spikes_out, float* preact_out, int64_t T,
+                                    int64_t R, int64_t K, int64_t N, float decay,
+                                    float in_scale, float v_threshold, float v_reset,
+                                    int32_t soft_reset, int32_t tile_hint, void* stream) {
+  if (T == 0 || R == 0) return (T < 0 || R < 0) ? SNNK_EINVAL : SNNK_OK;
+  ConvArgs a;
+  int st = linear_args(x, w, bias, spikes_out, preact_out, T, R, K, N, decay, in_scale,
+                       v_threshold, v_reset, soft_reset, true, &a);
+  if (st != SNNK_OK) return st;
+  return run<1>(a, false, tile_hint, 1, false, nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int snnk_linear_bias_lif_ws(const uint16_t* x, const uint16_t* w, const float* bias,
+                                       uint16_t* spikes_out, float* preact_out, int64_t T,
+                                       int64_t R, int64_t K, int64_t N, float decay,
+                                       float in_scale, float v_threshold, float v_reset,
+                                       int32_t soft_reset, int32_t tile_hint, int32_t splits,
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
+  if (T == 0 || R == 0) return (T < 0 || R < 0) ? SNNK_EINVAL : SNNK_OK;
+  ConvArgs a;
+  int st = linear_args(x, w, bias, spikes_out, preact_out, T, R, K, N, decay, in_scale,
+                       v_threshold, v_reset, soft_reset, true, &a);
+  if (st != SNNK_OK) return st;
+  return run<1>(a, false, tile_hint, splits, true, workspace, workspace_bytes,
+                static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t snnk_linear_bias_lif_ws_size(int64_t T, int64_t R, int64_t K, int64_t N,
+                                                int32_t preact, int32_t tile_hint,
+                                                int32_t splits) {
+  if (T == 0 || R == 0) return (T < 0 || R < 0) ? SNNK_EINVAL : 0;
+  ConvArgs a;
+  float dummy = 0.0f;
+  int st = linear_args(nullptr, nullptr, nullptr, nullptr, preact ? &dummy : nullptr, T, R, K,
+                       N, 0.f, 0.f, 0.f, 0.f, 0, false, &a);
+  if (st != SNNK_OK) return st;
+  Plan p;
+  st = make_plan(a, tile_hint, splits, true, &p);
+  return st != SNNK_OK ? st : p.ws_bytes;
 }

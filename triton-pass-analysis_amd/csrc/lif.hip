@@ -256,6 +256,7 @@ extern "C" const char* snnk_status_string(int status) {
     case SNNK_EINVAL: return "invalid argument";
     case SNNK_EUNSUPPORTED: return "unsupported configuration";
     case SNNK_EALIGN: return "misaligned pointer";
+    case SNNK_EWORKSPACE: return "workspace missing or too small";
     default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown status";
   }
 }

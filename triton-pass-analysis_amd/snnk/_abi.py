@@ -17,7 +17,7 @@ import torch
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libsnnk.so"
 
 # status codes (include/snnk.h)
-OK, EINVAL, EUNSUPPORTED, EALIGN = 0, -1, -2, -3
+OK, EINVAL, EUNSUPPORTED, EALIGN, EWORKSPACE = 0, -1, -2, -3, -4
 # element types
 F32, BF16, F16, U8, I32 = 0, 1, 2, 3, 4
 # spike formats
@@ -75,6 +75,25 @@ PROTOTYPES: dict[str, list] = {
         _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
         _i32, _i32, _p,        # soft_reset, tile_hint, stream
     ],
+    "snnk_conv3x3_bn_lif_ws": [
+        _p, _p, _p,            # x, w, bias
+        _p, _p,                # spikes_out, preact_out
+        _i64, _i64, _i64, _i64,  # T, B, H, W
+        _i64, _i64, _i32,      # Cin, Cout, pool
+        _f32, _f32, _f32,      # decay, in_scale, v_threshold
+        _f32, _i32, _i32,      # v_reset, soft_reset, tile_hint
+        _i32, _p, _i64,        # splits, workspace, workspace_bytes
+        _p,                    # stream
+    ],
+    "snnk_linear_bias_lif_ws": [
+        _p, _p, _p,            # x, w, bias
+        _p, _p,                # spikes_out, preact_out
+        _i64, _i64, _i64, _i64,  # T, R, K, N
+        _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
+        _i32, _i32,            # soft_reset, tile_hint
+        _i32, _p, _i64,        # splits, workspace, workspace_bytes
+        _p,                    # stream
+    ],
     "snnk_spike_attention": [
         _p, _p, _p,            # q, k, v
         _i64, _i64, _i64,      # q_row, k_row, v_row
@@ -97,6 +116,14 @@ PROTOTYPES: dict[str, list] = {
         _i64, _i64, _i64,      # N, C, HW
         _p,                    # stream
     ],
+}
+
+# entry points returning int64 (workspace bytes, or a negative status)
+SIZE_PROTOTYPES: dict[str, list] = {
+    "snnk_conv3x3_bn_lif_ws_size": [_i64, _i64, _i64, _i64, _i64, _i64,  # T, B, H, W, Cin, Cout
+                                    _i32, _i32, _i32, _i32],           # pool, preact, tile, splits
+    "snnk_linear_bias_lif_ws_size": [_i64, _i64, _i64, _i64,            # T, R, K, N
+                                     _i32, _i32, _i32],                 # preact, tile, splits
 }
 
 _lib = None
@@ -127,6 +154,10 @@ def lib():
         for name, argtypes in PROTOTYPES.items():
             fn = getattr(h, name)
             fn.restype = C.c_int
+            fn.argtypes = argtypes
+        for name, argtypes in SIZE_PROTOTYPES.items():
+            fn = getattr(h, name)
+            fn.restype = C.c_int64
             fn.argtypes = argtypes
         _lib = h
     return _lib
@@ -160,3 +191,11 @@ def dtype_code(dt: torch.dtype) -> int:
         return _DT[dt]
     except KeyError:
         raise AssertionError(f"unsupported dtype {dt}") from None
+
+
+def size_call(name: str, *args) -> int:
+    """Call an int64-returning entry point; negative results raise SnnkError."""
+    n = getattr(lib(), name)(*args)
+    if n < 0:
+        check(int(n), name)
+    return int(n)

@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import torch
 
-from .. import _abi
+from .. import _abi, _workspace
 from .fused import fold_conv_bn
 from .neurons import neuron_params
 
@@ -45,8 +45,12 @@ def to_nhwc_bf16(x_seq: torch.Tensor) -> torch.Tensor:
 def conv3x3_bn_lif_nhwc(x: torch.Tensor, w_prep: torch.Tensor, bias: torch.Tensor | None, *,
                         pool: bool, decay: float, in_scale: float, v_threshold: float,
                         v_reset: float = 0.0, soft_reset: bool = False,
-                        out: torch.Tensor | None = None, tile_hint: int = -1) -> torch.Tensor:
-    """NHWC bf16 spikes in, NHWC bf16 spikes out ([T, B, Ho, Wo, Cout])."""
+                        out: torch.Tensor | None = None, tile_hint: int = -1,
+                        splits: int | None = None) -> torch.Tensor:
+    """NHWC bf16 spikes in, NHWC bf16 spikes out ([T, B, Ho, Wo, Cout]).
+
+    ``splits``: K split over workgroups per output tile (None: chosen from the
+    shape, 1: never), reduced deterministically in the device workspace."""
     assert x.is_cuda and x.dtype == torch.bfloat16 and x.ndim == 5 and x.is_contiguous()
     T, B, H, W, Cin = x.shape
     Cout = w_prep.shape[0]
@@ -60,26 +64,37 @@ def conv3x3_bn_lif_nhwc(x: torch.Tensor, w_prep: torch.Tensor, bias: torch.Tenso
     else:
         assert out.shape == (T, B, Ho, Wo, Cout) and out.dtype == torch.bfloat16 \
             and out.is_contiguous()
-    with torch.cuda.device(x.device):
-        _abi.call("snnk_conv3x3_bn_lif", x.data_ptr(), w_prep.data_ptr(), _abi.ptr(bias),
-                  out.data_ptr(), None, T, B, H, W, Cin, Cout, 1 if pool else 0,
-                  float(decay), float(in_scale), float(v_threshold), float(v_reset),
-                  1 if soft_reset else 0, int(tile_hint), _abi.stream(x.device))
+    _conv_call(x, w_prep, bias, out, None, pool, decay, in_scale, v_threshold, v_reset,
+               soft_reset, tile_hint, splits)
     return out
 
 
+def _conv_call(x, w_prep, bias, out, pre, pool, decay, in_scale, v_threshold, v_reset,
+               soft_reset, tile_hint, splits):
+    T, B, H, W, Cin = x.shape
+    Cout = w_prep.shape[0]
+    sp = 0 if splits is None else int(splits)
+    with torch.cuda.device(x.device):
+        nbytes = _abi.size_call("snnk_conv3x3_bn_lif_ws_size", T, B, H, W, Cin, Cout,
+                                1 if pool else 0, 1 if pre is not None else 0,
+                                int(tile_hint), sp)
+        ws = _workspace.get(x.device, nbytes)
+        _abi.call("snnk_conv3x3_bn_lif_ws", x.data_ptr(), w_prep.data_ptr(), _abi.ptr(bias),
+                  _abi.ptr(out), _abi.ptr(pre), T, B, H, W, Cin, Cout, 1 if pool else 0,
+                  float(decay), float(in_scale), float(v_threshold), float(v_reset),
+                  1 if soft_reset else 0, int(tile_hint), sp, _abi.ptr(ws),
+                  0 if ws is None else ws.numel(), _abi.stream(x.device))
+
+
 def conv3x3_preact_nhwc(x: torch.Tensor, w_prep: torch.Tensor, bias: torch.Tensor | None,
-                        *, tile_hint: int = -1) -> torch.Tensor:
+                        *, tile_hint: int = -1, splits: int | None = None) -> torch.Tensor:
     """fp32 conv + bias, NHWC ``[T, B, H, W, Cout]`` (the membrane input, no LIF)."""
     assert x.is_cuda and x.dtype == torch.bfloat16 and x.ndim == 5 and x.is_contiguous()
     T, B, H, W, Cin = x.shape
     Cout = w_prep.shape[0]
     assert w_prep.shape == (Cout, 9 * Cin) and w_prep.dtype == torch.bfloat16
     pre = torch.empty(T, B, H, W, Cout, device=x.device, dtype=torch.float32)
-    with torch.cuda.device(x.device):
-        _abi.call("snnk_conv3x3_bn_lif", x.data_ptr(), w_prep.data_ptr(), _abi.ptr(bias),
-                  None, pre.data_ptr(), T, B, H, W, Cin, Cout, 0, 1.0, 1.0, 1.0, 0.0, 0,
-                  int(tile_hint), _abi.stream(x.device))
+    _conv_call(x, w_prep, bias, None, pre, False, 1.0, 1.0, 1.0, 0.0, False, tile_hint, splits)
     return pre
 
 

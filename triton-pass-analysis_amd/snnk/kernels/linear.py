@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import torch
 
-from .. import _abi
+from .. import _abi, _workspace
 
 
 def linear_fusable(x_seq: torch.Tensor, weight: torch.Tensor, v_threshold) -> bool:
@@ -34,8 +34,11 @@ def _check(x, w, bias):
 def linear_bias_lif(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
                     decay: float, in_scale: float, v_threshold: float, v_reset: float = 0.0,
                     soft_reset: bool = False, out: torch.Tensor | None = None,
-                    tile_hint: int = -1) -> torch.Tensor:
-    """x [T, R, K] bf16, w [N, K] bf16 -> spikes [T, R, N] bf16."""
+                    tile_hint: int = -1, splits: int | None = None) -> torch.Tensor:
+    """x [T, R, K] bf16, w [N, K] bf16 -> spikes [T, R, N] bf16.
+
+    ``splits``: K split over workgroups per output tile (None: chosen from the
+    shape, 1: never), reduced deterministically in the device workspace."""
     _check(x, w, bias)
     T, R, K = x.shape
     N = w.shape[0]
@@ -43,16 +46,29 @@ def linear_bias_lif(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None,
         out = torch.empty(T, R, N, device=x.device, dtype=torch.bfloat16)
     else:
         assert out.shape == (T, R, N) and out.dtype == torch.bfloat16 and out.is_contiguous()
-    with torch.cuda.device(x.device):
-        _abi.call("snnk_linear_bias_lif", x.data_ptr(), w.data_ptr(), _abi.ptr(bias),
-                  out.data_ptr(), None, T, R, K, N, float(decay), float(in_scale),
-                  float(v_threshold), float(v_reset), 1 if soft_reset else 0, int(tile_hint),
-                  _abi.stream(x.device))
+    _linear_call(x, w, bias, out, None, decay, in_scale, v_threshold, v_reset, soft_reset,
+                 tile_hint, splits)
     return out
 
 
+def _linear_call(x, w, bias, out, pre, decay, in_scale, v_threshold, v_reset, soft_reset,
+                 tile_hint, splits):
+    T, R, K = x.shape
+    N = w.shape[0]
+    sp = 0 if splits is None else int(splits)
+    with torch.cuda.device(x.device):
+        nbytes = _abi.size_call("snnk_linear_bias_lif_ws_size", T, R, K, N,
+                                1 if pre is not None else 0, int(tile_hint), sp)
+        ws = _workspace.get(x.device, nbytes)
+        _abi.call("snnk_linear_bias_lif_ws", x.data_ptr(), w.data_ptr(), _abi.ptr(bias),
+                  _abi.ptr(out), _abi.ptr(pre), T, R, K, N, float(decay), float(in_scale),
+                  float(v_threshold), float(v_reset), 1 if soft_reset else 0, int(tile_hint),
+                  sp, _abi.ptr(ws), 0 if ws is None else ws.numel(), _abi.stream(x.device))
+
+
 def linear_preact(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
-                  out: torch.Tensor | None = None, tile_hint: int = -1) -> torch.Tensor:
+                  out: torch.Tensor | None = None, tile_hint: int = -1,
+                  splits: int | None = None) -> torch.Tensor:
     """x [T, R, K] bf16, w [N, K] bf16 -> fp32 x.w^T + bias [T, R, N] (no neuron)."""
     _check(x, w, bias)
     T, R, K = x.shape
@@ -61,8 +77,5 @@ def linear_preact(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *
         out = torch.empty(T, R, N, device=x.device, dtype=torch.float32)
     else:
         assert out.shape == (T, R, N) and out.dtype == torch.float32 and out.is_contiguous()
-    with torch.cuda.device(x.device):
-        _abi.call("snnk_linear_bias_lif", x.data_ptr(), w.data_ptr(), _abi.ptr(bias),
-                  None, out.data_ptr(), T, R, K, N, 1.0, 1.0, 1.0, 0.0, 0, int(tile_hint),
-                  _abi.stream(x.device))
+    _linear_call(x, w, bias, None, out, 1.0, 1.0, 1.0, 0.0, False, tile_hint, splits)
     return out
