@@ -4,8 +4,9 @@
 //   C[b][m][n] = 2 * sum_k A01*B01 - sum_k A01[m][k]         (signed weights)
 // with A, B packed along k as uint32 words (bit k%32 of word k/32).
 //
-// Each wave owns a 128x128 tile of C as 4x4 MFMA 32x32 accumulators and walks
-// K in stages of 4 words (128 bits).  Packed words are loaded straight into
+// Each wave owns a (32*TM)x(32*TN) tile of C as TMxTN MFMA 32x32 accumulators
+// and walks K in stages of 4 words (128 bits).  With TM x TN = 4 x 2 two
+// waves fit a SIMD, so one wave's result stores overlap the other's MFMAs.  Packed words are loaded straight into
 // registers one stage ahead; no LDS.  A packed 32-bit word feeds one MFMA
 // k-step (32 int8 k values): the lane half g (lane/32) builds its 16 operand
 // bytes as the 4 dwords (w >> (4g+s)) & 0x01010101, s = 0..3, i.e. byte b of
@@ -26,34 +27,12 @@ namespace {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kTile = 128;     // per wave, square
 constexpr int kStageW = 4;     // packed words per stage
 
-// Four packed words of a row starting at word w0, all inside the row.
-template <bool VEC>
-__device__ __forceinline__ u32x4 load_full(const uint32_t* row, int64_t w0) {
-  if constexpr (VEC) {
-    return *reinterpret_cast<const u32x4*>(row + w0);
-  } else {
-    u32x4 v;
-    v[0] = row[w0]; v[1] = row[w0 + 1]; v[2] = row[w0 + 2]; v[3] = row[w0 + 3];
-    return v;
-  }
-}
-
-// The last (partial) stage: words past KW read as 0, the last word masked.
-__device__ __forceinline__ u32x4 load_tail(const uint32_t* row, int64_t w0, int64_t KW,
-                                           uint32_t last_mask) {
-  u32x4 v = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int j = 0; j < kStageW; ++j) {
-    if (w0 + j < KW) {
-      uint32_t x = row[w0 + j];
-      v[j] = (w0 + j == KW - 1) ? (x & last_mask) : x;
-    }
-  }
-  return v;
-}
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+constexpr uint32_t kOOB = 0xFFFFFFF0u;        // buffer offset past every operand
+constexpr int kRsrcWord3 = 0x00020000;       // raw buffer, 32-bit data format
+constexpr int kRing = 8;                     // stages in the LDS ring
 
 __device__ __forceinline__ i32x4 expand(uint32_t w, int g) {
   const uint32_t x = w >> (4 * g);
@@ -65,100 +44,131 @@ __device__ __forceinline__ i32x4 expand(uint32_t w, int g) {
   return r;
 }
 
-// 4 MFMA k-steps of one stage for the wave's 4x4 accumulator tiles.
-template <bool SIGNED>
-__device__ __forceinline__ void mfma_stage(i32x16 (&acc)[4][4], const u32x4 (&a)[4],
-                                           const u32x4 (&b)[4], int g, int (&rowpop)[4]) {
+// 4 MFMA k-steps of one stage for the wave's TM x TN accumulator tiles.
+template <bool SIGNED, int TM, int TN>
+__device__ __forceinline__ void mfma_stage(i32x16 (&acc)[TM][TN], const u32x4 (&a)[TM],
+                                           const u32x4 (&b)[TN], int g, int (&rowpop)[TM]) {
 #pragma unroll
   for (int kk = 0; kk < kStageW; ++kk) {
-    i32x4 fa[4], fb[4];
+    i32x4 fa[TM], fb[TN];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < TM; ++t) {
       fa[t] = expand(a[t][kk], g);
-      fb[t] = expand(b[t][kk], g);
       if constexpr (SIGNED) rowpop[t] += __builtin_popcount(a[t][kk]);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int t = 0; t < TN; ++t) fb[t] = expand(b[t][kk], g);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
   }
 }
 
-// n_main stages of 4 full words run without guards; a final partial stage
-// (KW % 4 != 0, or a masked last word) runs once with guards.
-template <bool SIGNED, bool OUT_F32, bool VEC>
+// One wave per workgroup.  The packed words of each stage (4 per row: 16
+// bytes for each of the 32*TM A rows and 32*TN B rows) arrive by direct
+// global->LDS buffer loads into a kRing-deep ring, kRing-1 stages ahead, so
+// no barrier is needed (one wave) and the load latency stays hidden.  Rows
+// past M / N read as zeros (range-checked offsets); in the last stage words
+// past KW are cleared and the bits past K of the last word masked.
+template <bool SIGNED, bool OUT_F32, int TM, int TN>
 __global__ __launch_bounds__(64) void bgemm_mfma_kernel(
     const uint32_t* __restrict__ A, const uint32_t* __restrict__ B, void* __restrict__ Cv,
-    int64_t M, int64_t N, int64_t KW, int64_t n_main, int has_tail, uint32_t last_mask,
-    int64_t lda, int64_t ldb, int64_t ldc, int64_t sA, int64_t sB, int64_t sC) {
+    int64_t M, int64_t N, int64_t KW, uint32_t last_mask, int64_t lda, int64_t ldb,
+    int64_t ldc, int64_t sA, int64_t sB, int64_t sC, uint32_t a_bytes, uint32_t b_bytes) {
+  constexpr int kRows = 32 * (TM + TN);          // rows per stage, A then B
+  __shared__ __attribute__((aligned(1024))) u32x4 ring[kRing][kRows];
   const int lane = threadIdx.x;
   const int r32 = lane & 31, g = lane >> 5;
   const int64_t bz = blockIdx.z;
-  const int64_t m_base = static_cast<int64_t>(blockIdx.y) * kTile;
-  const int64_t n_base = static_cast<int64_t>(blockIdx.x) * kTile;
-  A += bz * sA;
-  B += bz * sB;
+  const int64_t m_base = static_cast<int64_t>(blockIdx.y) * (32 * TM);
+  const int64_t n_base = static_cast<int64_t>(blockIdx.x) * (32 * TN);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(A + bz * sA), 0, a_bytes, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(B + bz * sB), 0, b_bytes, kRsrcWord3);
 
-  // Rows past M / N read row 0: they only feed outputs that are never stored.
-  const uint32_t* arow[4];
-  const uint32_t* brow[4];
+  // lane l loads row 64*q + l of the stage (q-th 64-row group)
+  constexpr int kGroups = kRows / 64;
+  uint32_t row_off[kGroups];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int64_t m = m_base + t * 32 + r32, n = n_base + t * 32 + r32;
-    arow[t] = A + (m < M ? m : 0) * lda;
-    brow[t] = B + (n < N ? n : 0) * ldb;
+  for (int q = 0; q < kGroups; ++q) {
+    const int r = 64 * q + lane;
+    if (r < 32 * TM) {
+      const int64_t m = m_base + r;
+      row_off[q] = m < M ? static_cast<uint32_t>(m * lda * 4) : kOOB;
+    } else {
+      const int64_t n = n_base + (r - 32 * TM);
+      row_off[q] = n < N ? static_cast<uint32_t>(n * ldb * 4) : kOOB;
+    }
   }
+  const int64_t n_stages = (KW + kStageW - 1) / kStageW;
+  auto issue = [&](int64_t st, int buf) {
+    const bool live = st < n_stages;
+    const uint32_t d = static_cast<uint32_t>(st * kStageW * 4);
+#pragma unroll
+    for (int q = 0; q < kGroups; ++q) {
+      const bool is_a = 64 * q < 32 * TM;  // compile-time after unrolling
+      const uint32_t off = (live && row_off[q] != kOOB) ? row_off[q] + d : kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? ra : rb, (lds_ptr_t)&ring[buf][64 * q], 16,
+                                               off, 0, 0, 0);
+    }
+  };
 
-  i32x16 acc[4][4];
+  i32x16 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
-  int rowpop[4] = {0, 0, 0, 0};
+  int rowpop[TM];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) rowpop[t] = 0;
 
-  // Stage s < n_main holds 4 full words; stage n_main (if has_tail) is the
-  // guarded partial stage.  The loads of stage s+1 are issued before stage s
-  // runs on the MFMA pipe; one MFMA block serves every stage.
-  const int64_t n_stages = n_main + has_tail;
-  u32x4 a_cur[4], b_cur[4];
-  auto load_stage = [&](u32x4 (&a)[4], u32x4 (&b)[4], int64_t st) {
-    const int64_t w0 = st * kStageW;
-    if (st < n_main) {
+  // operands of stage st from its ring slot; the last stage clears words past
+  // KW and masks the bits past K (uniform branch)
+  auto read_stage = [&](u32x4 (&a)[TM], u32x4 (&b)[TN], int64_t st) {
+    const int rb_ = static_cast<int>(st % kRing);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        a[t] = load_full<VEC>(arow[t], w0);
-        b[t] = load_full<VEC>(brow[t], w0);
-      }
-    } else if (st < n_stages) {
+    for (int t = 0; t < TM; ++t) a[t] = ring[rb_][t * 32 + r32];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        a[t] = load_tail(arow[t], w0, KW, last_mask);
-        b[t] = load_tail(brow[t], w0, KW, last_mask);
+    for (int t = 0; t < TN; ++t) b[t] = ring[rb_][32 * TM + t * 32 + r32];
+    if (st == n_stages - 1) {
+      const int64_t w0 = st * kStageW;
+#pragma unroll
+      for (int j = 0; j < kStageW; ++j) {
+        const uint32_t keep = w0 + j < KW - 1 ? 0xFFFFFFFFu : (w0 + j == KW - 1 ? last_mask : 0u);
+#pragma unroll
+        for (int t = 0; t < TM; ++t) a[t][j] &= keep;
+#pragma unroll
+        for (int t = 0; t < TN; ++t) b[t][j] &= keep;
       }
     }
   };
-  load_stage(a_cur, b_cur, 0);
-  for (int64_t s = 0; s < n_stages; ++s) {
-    u32x4 a_nxt[4], b_nxt[4];
-    load_stage(a_nxt, b_nxt, s + 1);
-    mfma_stage<SIGNED>(acc, a_cur, b_cur, g, rowpop);
+
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      a_cur[t] = a_nxt[t];
-      b_cur[t] = b_nxt[t];
-    }
+  for (int p = 0; p < kRing - 1; ++p) issue(p, p);
+  for (int64_t s = 0; s < n_stages; ++s) {
+    // stage s has landed once at most the kRing-2 stages after it are
+    // outstanding (each stage is kGroups loads per lane)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kGroups * (kRing - 2)) : "memory");
+    u32x4 a[TM], b[TN];
+    read_stage(a, b, s);
+    // refill the slot of stage s-1: its reads completed before last stage's
+    // MFMAs consumed them (one wave per block, so no barrier)
+    issue(s + kRing - 1, static_cast<int>((s + kRing - 1) % kRing));
+    mfma_stage<SIGNED, TM, TN>(acc, a, b, g, rowpop);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing zero-fill loads
 
   // Epilogue.  Accumulator register e of lane l holds row 8*(e/4) + 4*g + e%4,
   // column l%32 of its 32x32 tile.
   void* Cb = OUT_F32 ? static_cast<void*>(static_cast<float*>(Cv) + bz * sC)
                      : static_cast<void*>(static_cast<int32_t*>(Cv) + bz * sC);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int rr = 8 * (e >> 2) + 4 * g + (e & 3);
@@ -166,7 +176,7 @@ __global__ __launch_bounds__(64) void bgemm_mfma_kernel(
       if constexpr (SIGNED) rp = __shfl(rowpop[i], rr, 64);
       const int64_t m = m_base + i * 32 + rr;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < TN; ++j) {
         const int64_t n = n_base + j * 32 + r32;
         if (m < M && n < N) {
           int32_t c = acc[i][j][e];
@@ -181,27 +191,21 @@ __global__ __launch_bounds__(64) void bgemm_mfma_kernel(
   }
 }
 
-template <bool SIGNED, bool OUT_F32>
+template <bool SIGNED, bool OUT_F32, int TM = 4, int TN = 4>
 int launch_mfma(const uint32_t* A, const uint32_t* B, void* C, int64_t batch, int64_t M,
                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t sA,
                 int64_t sB, int64_t sC, hipStream_t stream) {
   const int64_t KW = (K + 31) / 32;
   const uint32_t last_mask = (K % 32) ? ((1u << (K % 32)) - 1u) : 0xFFFFFFFFu;
-  const bool has_tail = (KW % kStageW != 0) || (last_mask != 0xFFFFFFFFu);
-  const int64_t n_main = has_tail ? KW / kStageW - ((KW % kStageW == 0) ? 1 : 0) : KW / kStageW;
-  const int64_t gx = (N + kTile - 1) / kTile, gy = (M + kTile - 1) / kTile;
+  const int64_t gx = (N + 32 * TN - 1) / (32 * TN), gy = (M + 32 * TM - 1) / (32 * TM);
   if (gx > 0x7FFFFFFFll || gy > 65535 || batch > 65535) return SNNK_EUNSUPPORTED;
-  // 16-byte row loads need 16-byte aligned rows
-  const bool vec = aligned(A, 16) && aligned(B, 16) && (lda % 4 == 0) && (ldb % 4 == 0) &&
-                   (batch == 1 || ((sA % 4 == 0) && (sB % 4 == 0)));
-  if (vec)
-    hipLaunchKernelGGL((bgemm_mfma_kernel<SIGNED, OUT_F32, true>), dim3(gx, gy, batch), dim3(64),
-                       0, stream, A, B, C, M, N, KW, n_main, has_tail ? 1 : 0, last_mask, lda,
-                       ldb, ldc, sA, sB, sC);
-  else
-    hipLaunchKernelGGL((bgemm_mfma_kernel<SIGNED, OUT_F32, false>), dim3(gx, gy, batch), dim3(64),
-                       0, stream, A, B, C, M, N, KW, n_main, has_tail ? 1 : 0, last_mask, lda,
-                       ldb, ldc, sA, sB, sC);
+  // byte offsets within one batch's operand are 32-bit (buffer descriptors)
+  const int64_t a_bytes = ((M - 1) * lda + KW) * 4, b_bytes = ((N - 1) * ldb + KW) * 4;
+  if (a_bytes + 16 > kOOB || b_bytes + 16 > kOOB) return SNNK_EUNSUPPORTED;
+  if (!aligned(A, 4) || !aligned(B, 4)) return SNNK_EALIGN;
+  hipLaunchKernelGGL((bgemm_mfma_kernel<SIGNED, OUT_F32, TM, TN>), dim3(gx, gy, batch), dim3(64),
+                     0, stream, A, B, C, M, N, KW, last_mask, lda, ldb, ldc, sA, sB, sC,
+                     static_cast<uint32_t>(a_bytes), static_cast<uint32_t>(b_bytes));
   return launch_status();
 }
 
