@@ -25,10 +25,12 @@
 // Longer T runs in chunks of 4 steps with the membrane kept in registers.
 //
 // A block is WM x WN x KS waves.  Each wave owns TM x TN accumulator tiles;
-// the KS wave groups take interleaved 32-wide K stages of the same output
-// tile (group g: stages g, g+KS, ...; a group past the last stage loads
-// zeros) and are summed through LDS before the epilogue (split-K for the
-// small late layers).  Operand stages are double buffered in LDS.
+// the KS wave groups take interleaved 64-wide K stages of the same output
+// tile (group g: stages g, g+KS, ...) and are summed through LDS before the
+// epilogue (split-K for the small late layers); blocks may also split K
+// across the grid (partials in a workspace).  Operand stages stream through
+// an NBUF-deep LDS ring filled by direct global->LDS buffer loads; each
+// lane's source offsets are rebuilt only when the stage's tap changes.
 #include <algorithm>
 
 #include "snnk_common.h"
@@ -46,7 +48,11 @@ constexpr int kRow = kKS;         // LDS row pitch in bf16 (128 B, eight 16-byte
 constexpr int kRowBytes = kRow * 2;
 constexpr int kDmaRows = 1024 / kRowBytes;  // rows filled by one wave-wide 16-byte load
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
-constexpr uint32_t kOOB = 0xFFFFFFF0u;  // buffer offset past every operand (reads zeros)
+// Offset base past every operand: kFar plus any stage delta (< 2^31) stays
+// below 2^32 and at or past the end of an operand of at most kFar bytes, so
+// such a load reads zeros (padding taps, rows past the end, steps past T,
+// columns past Cout, the half of a last stage past K).
+constexpr uint32_t kFar = 0x80000000u;
 
 // Wait until at most N of this wave's vector-memory loads are outstanding,
 // then meet the other waves of the block.  Written out so that no release
@@ -54,6 +60,18 @@ constexpr uint32_t kOOB = 0xFFFFFFF0u;  // buffer offset past every operand (rea
 template <int N>
 __device__ __forceinline__ void wait_vmcnt_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Wait for a ring stage whose `later` successors (at most MAXL, kSEG loads
+// each) may still be in flight; a stage past the end issues no loads, so the
+// tail of the K loop waits for fewer.
+template <int kSEG, int MAXL>
+__device__ __forceinline__ void wait_stages_barrier(int later) {
+  static_assert(MAXL >= 0 && MAXL <= 3, "ring depth");
+  if (later >= MAXL) wait_vmcnt_barrier<kSEG * MAXL>();
+  else if (later == 2) wait_vmcnt_barrier<kSEG * 2>();
+  else if (later == 1) wait_vmcnt_barrier<kSEG>();
+  else wait_vmcnt_barrier<0>();
 }
 
 // 16-byte chunk c of LDS row r is stored at chunk c ^ key(r).  gfx950 serves
@@ -76,9 +94,10 @@ struct ConvArgs {
   int n_quads;        // quads in one time step
   int n_stages;       // K / 32
   FastDiv div_cin;
+  FastDiv div_howo, div_wo, div_hw, div_w;  // row index -> (b, y, x)
   uint32_t x_tstride_b;  // bytes of one input step (B*H*W*Cin*2)
-  uint32_t x_bytes;      // bytes of x (T steps), below kOOB
-  uint32_t w_bytes;      // bytes of w, below kOOB
+  uint32_t x_bytes;      // bytes of x (T steps), at most kFar
+  uint32_t w_bytes;      // bytes of w, at most kFar
   int64_t o_tstride;     // B*Ho*Wo*Cout
   int tiles_m, tiles_n;  // output tiles along rows (quads) and Cout
   // cross-block split-K: `splits` blocks share one output tile, each over
@@ -180,12 +199,15 @@ void conv3x3_kernel(ConvArgs a) {
   // q is B rows kDmaRows*q..; wave wmn of the group loads A segments
   // wmn + i*kGroupWaves (i < kAPer) and the same B segments (i < kBPer).
   // Lane l writes row kDmaRows*q + l/8, chunk slot l%8, and so reads source
-  // chunk c = slot ^ key(row).  Chunks 0-3 hold k0..k0+31 of the stage, chunks 4-7
-  // k0+32..k0+63; with Cin % 64 == 32 the halves may fall in different taps.
+  // chunk c = slot ^ key(row).  Chunks 0-3 hold k0..k0+31 of the stage, chunks
+  // 4-7 k0+32..k0+63: the lane's half is h = c/4, and since key(row) has bit
+  // 2 = (q ^ row) & 1, h = h0 ^ (q & 1) with h0 = (slot/4) ^ (l/8 & 1).  With
+  // Cin % 64 == 32 the two halves of a stage may fall in different taps.
   const int lrow = lane >> 3, slot = lane & 7;
-  uint32_t s_base[C::kSegPer];  // A: bytes of (t, b, y, x, chunk % 4); B: bytes of (n, chunk)
-  uint32_t s_mask[C::kSegPer];  // A: bit tap = source pixel in the image, bit 31 = upper half;
-                                // B: bit 0 = n < Cout, bits 4-6 = chunk
+  const uint32_t h0 = static_cast<uint32_t>((slot >> 2) ^ (lrow & 1));
+  uint32_t s_base[C::kSegPer];  // A: bytes of (t, b, y, x) + 16*(c%4); B: bytes of (n, c) or kFar
+  uint32_t s_ok[C::kAPer];      // A: bit tap set when the row exists and the tap's source
+                                // pixel is inside the image
 #pragma unroll
   for (int i = 0; i < C::kSegPer; ++i) {
     if (i < C::kAPer) {
@@ -196,40 +218,46 @@ void conv3x3_kernel(ConvArgs a) {
       const int quad = quad0 + (r >> 5) * 2 + gr;
       int b = 0, y = 0, xx = 0;
       const bool row_ok = quad < a.n_quads;
+      uint32_t ok = 0;
       if (row_ok) {
         if constexpr (POOL) {
-          const int howo = a.Ho * a.Wo;
-          b = quad / howo;
-          const int r2 = quad - b * howo;
-          const int py = r2 / a.Wo, px = r2 - py * a.Wo;
+          b = static_cast<int>(fdiv(static_cast<uint32_t>(quad), a.div_howo));
+          const int r2 = quad - b * a.Ho * a.Wo;
+          const int py = static_cast<int>(fdiv(static_cast<uint32_t>(r2), a.div_wo));
+          const int px = r2 - py * a.Wo;
           y = 2 * py + (pq >> 1);
           xx = 2 * px + (pq & 1);
         } else {
-          const int p = quad * 4 + pq;
-          b = p / HW;
-          const int r2 = p - b * HW;
-          y = r2 / a.W;
+          const int pix = quad * 4 + pq;
+          b = static_cast<int>(fdiv(static_cast<uint32_t>(pix), a.div_hw));
+          const int r2 = pix - b * HW;
+          y = static_cast<int>(fdiv(static_cast<uint32_t>(r2), a.div_w));
           xx = r2 - y * a.W;
         }
-      }
-      uint32_t ok = 0;
-#pragma unroll
-      for (int tap = 0; tap < TAPS; ++tap) {
-        const int ys = y + tap_dy<TAPS>(tap), xs = xx + tap_dx<TAPS>(tap);
-        if (row_ok && ys >= 0 && ys < a.H && xs >= 0 && xs < a.W) ok |= 1u << tap;
+        if constexpr (TAPS == 9) {
+          // tap kh*3 + kw reads (y + kh - 1, x + kw - 1)
+          const uint32_t vx = (xx > 0 ? 1u : 0u) | 2u | (xx + 1 < a.W ? 4u : 0u);
+          ok = (y > 0 ? vx : 0u) | (vx << 3) | (y + 1 < a.H ? vx << 6 : 0u);
+        } else {
+          ok = 1u;
+        }
       }
       const int c = swz(r, slot);
       s_base[i] = static_cast<uint32_t>(t) * a.x_tstride_b +
                   static_cast<uint32_t>(((b * a.H + y) * a.W + xx) * a.Cin) * 2u + (c & 3) * 16u;
-      s_mask[i] = ok | (static_cast<uint32_t>(c >> 2) << 31);
+      s_ok[i] = ok;
     } else {
       const int n = kDmaRows * (wmn + (i - C::kAPer) * C::kGroupWaves) + lrow;
       const int c = swz(n, slot);
-      s_mask[i] = (n0 + n < a.Cout ? 1u : 0u) | (static_cast<uint32_t>(c) << 4);
-      s_base[i] = static_cast<uint32_t>(n0 + n) * static_cast<uint32_t>(K) * 2u + c * 16u;
+      s_base[i] = n0 + n < a.Cout
+                      ? static_cast<uint32_t>(n0 + n) * static_cast<uint32_t>(K) * 2u + c * 16u
+                      : kFar;
     }
   }
 
+  // every K group runs n_stages_g ring iterations (their barriers are
+  // shared); when the block's K stages do not split evenly over the groups,
+  // a group's last one lies past the block's range and is loaded as zeros
   const int n_stages_g = (st_end - st_begin + KSPLIT - 1) / KSPLIT;
   const int n_chunks = (a.T + 3) / 4;
 
@@ -313,57 +341,77 @@ void conv3x3_kernel(ConvArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // steps past T read zeros
-    uint32_t live_mask[C::kSegPer];
+    // Source offsets of this lane's A segments for the tap pair (tap_lo,
+    // tap_hi) of the stage last prepared: kFar where the row, the step or
+    // the tap's source pixel does not exist.  A stage then costs one add
+    // per segment; the offsets are rebuilt only when the tap pair changes.
     const bool t_ok = tc * 4 + (lrow & 3) < a.T;
-#pragma unroll
-    for (int i = 0; i < C::kSegPer; ++i)
-      live_mask[i] = (i >= C::kAPer || t_ok) ? s_mask[i] : 0u;  // no tap bit left: zeros
     const uint32_t chunk_off = static_cast<uint32_t>(tc) * 4u * a.x_tstride_b;
+    uint32_t a_off[C::kAPer];
+#pragma unroll
+    for (int i = 0; i < C::kAPer; ++i) a_off[i] = kFar;
+    int cur_lo = -1, cur_hi = -1;
 
-    // enqueue the direct global->LDS loads of group-local stage sl
     // wave-uniform addressing of group-local stage sl
     struct StageAddr {
-      bool live;
-      int tap_lo, tap_hi, k_left;
-      uint32_t d_lo, d_hi, b_delta;
+      bool live;        // a stage of the ring loop (later slots are not loaded)
+      bool zero_b;      // B reads zeros: a stage past the block's K range
+      bool tail;        // the last stage of K % 64 == 32: upper half past K
+      uint32_t da, db;  // A: chunk + channel bytes of the lower half; B: bytes of k0
     };
-    auto stage_addr = [&](int sl) {
+    auto prepare = [&](int sl) {
       StageAddr p;
       const int sg = st_begin + sl * KSPLIT + kg;
-      p.live = sg < st_end;
-      const int k0 = p.live ? sg * kKS : 0;
-      // tap and channel offset of each 32-wide half of the stage; a half at
-      // or past K gets tap TAPS, which no source pixel mask contains
-      p.tap_lo = static_cast<int>(fdiv(static_cast<uint32_t>(k0), a.div_cin));
-      p.tap_hi = static_cast<int>(fdiv(static_cast<uint32_t>(k0 + 32), a.div_cin));
-      const int cin_lo = k0 - p.tap_lo * a.Cin, cin_hi = k0 + 32 - p.tap_hi * a.Cin;
-      p.d_lo = chunk_off + static_cast<uint32_t>(
-          ((tap_dy<TAPS>(p.tap_lo) * a.W + tap_dx<TAPS>(p.tap_lo)) * a.Cin + cin_lo) * 2);
-      p.d_hi = chunk_off + static_cast<uint32_t>(
-          ((tap_dy<TAPS>(p.tap_hi) * a.W + tap_dx<TAPS>(p.tap_hi)) * a.Cin + cin_hi) * 2);
-      p.b_delta = static_cast<uint32_t>(k0) * 2u;
-      p.k_left = K - k0;  // chunk c of a B row is inside K when 8c < k_left
+      p.live = sl < n_stages_g;
+      p.zero_b = sg >= st_end;
+      const uint32_t k0 = p.zero_b ? 0u : static_cast<uint32_t>(sg * kKS);
+      const int tap_lo = static_cast<int>(fdiv(k0, a.div_cin));
+      const int cin_lo = static_cast<int>(k0) - tap_lo * a.Cin;
+      const bool wrap = cin_lo + 32 >= a.Cin;  // upper half starts the next tap
+      const int tap_hi = tap_lo + (wrap ? 1 : 0);
+      p.da = chunk_off + static_cast<uint32_t>(cin_lo) * 2u;
+      p.db = k0 * 2u;
+      p.tail = static_cast<int>(k0) + 32 >= K;
+      if (p.live && p.zero_b) {  // (rare) every A offset past the end as well
+        cur_lo = cur_hi = -1;
+        p.da = 0;
+#pragma unroll
+        for (int i = 0; i < C::kAPer; ++i) a_off[i] = kFar;
+      } else if (p.live && (tap_lo != cur_lo || tap_hi != cur_hi)) {
+        cur_lo = tap_lo;
+        cur_hi = tap_hi;
+        // byte delta of each half's source pixel, relative to p.da; the upper
+        // half sits 32 channels on, or at channel cin_lo + 32 - Cin of the
+        // next tap (a tap past the last has no ok bit: zeros)
+        const int32_t del_lo = (tap_dy<TAPS>(tap_lo) * a.W + tap_dx<TAPS>(tap_lo)) * a.Cin * 2;
+        const int32_t del_hi = (tap_dy<TAPS>(tap_hi) * a.W + tap_dx<TAPS>(tap_hi)) * a.Cin * 2 +
+                               64 - (wrap ? 2 * a.Cin : 0);
+#pragma unroll
+        for (int i = 0; i < C::kAPer; ++i) {
+          const uint32_t h = h0 ^ static_cast<uint32_t>((wmn + i * C::kGroupWaves) & 1);
+          const int tap = h ? tap_hi : tap_lo;
+          const bool ok = t_ok && ((s_ok[i] >> tap) & 1u);
+          a_off[i] = ok ? s_base[i] + static_cast<uint32_t>(h ? del_hi : del_lo) : kFar;
+        }
+      }
       return p;
     };
-    // enqueue the direct global->LDS load of segment i of a stage
+    // enqueue the direct global->LDS load of segment i of a stage (none for
+    // a ring slot past the loop)
     auto issue_seg = [&](const StageAddr& p, int i, int buf) {
+      if (!p.live) return;
       unsigned char* stage = smem + buf * C::kStageBytes;
-      const uint32_t m = live_mask[i];
-      const uint32_t live = p.live ? 1u : 0u;
       if (i < C::kAPer) {  // resolved at compile time
         const int q = wmn + i * C::kGroupWaves;
-        const uint32_t hi = m >> 31;
-        const int tap = hi ? p.tap_hi : p.tap_lo;
-        const uint32_t ok = live & (m >> tap);
-        const uint32_t off = (ok & 1u) ? s_base[i] + (hi ? p.d_hi : p.d_lo) : kOOB;
+        // (the offset goes through a variable: with the sum written in the
+        // call, hipcc's host pass drops the kernel's launch stub)
+        const uint32_t off = a_off[i] + p.da;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             xr, (lds_ptr_t)(stage + (kg * C::BM + kDmaRows * q) * kRowBytes), 16, off, 0, 0, 0);
       } else {
         const int q = wmn + (i - C::kAPer) * C::kGroupWaves;
-        const uint32_t in_k = static_cast<int>(8 * ((m >> 4) & 7u)) < p.k_left ? 1u : 0u;
-        const uint32_t ok = live & m & in_k;
-        const uint32_t off = (ok & 1u) ? s_base[i] + p.b_delta : kOOB;
+        uint32_t off = s_base[i] + p.db;
+        if (p.zero_b || (p.tail && (h0 ^ static_cast<uint32_t>(q & 1)))) off = kFar;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             wr, (lds_ptr_t)(stage + (KSPLIT * C::BM + kg * C::BN + kDmaRows * q) * kRowBytes),
             16, off, 0, 0, 0);
@@ -372,7 +420,7 @@ void conv3x3_kernel(ConvArgs a) {
 
 #pragma unroll
     for (int p = 0; p < C::kBuf - 1; ++p) {
-      const StageAddr sp = stage_addr(p);
+      const StageAddr sp = prepare(p);
 #pragma unroll
       for (int i = 0; i < C::kSegPer; ++i) issue_seg(sp, i, p);
     }
@@ -382,9 +430,10 @@ void conv3x3_kernel(ConvArgs a) {
       // this wave's loads of stage s are done once at most the later
       // stages' loads are outstanding; the barrier publishes every wave's
       // loads and retires the reads of the buffer refilled next
-      wait_vmcnt_barrier<C::kSegPer * (C::kBuf - 2)>();
+      wait_stages_barrier<C::kSegPer, C::kBuf - 2>(n_stages_g - 1 - s);
       const int nbuf = buf == 0 ? C::kBuf - 1 : buf - 1;
-      const StageAddr sp = stage_addr(s + C::kBuf - 1);
+      const StageAddr sp = prepare(s + C::kBuf - 1);
+
       const unsigned char* st = smem + buf * C::kStageBytes;
       const uint16_t* sa = reinterpret_cast<const uint16_t*>(st) + (kg * C::BM + wm * TM * 32 + r_lane) * kRow;
       const uint16_t* sb = reinterpret_cast<const uint16_t*>(st) +
@@ -418,7 +467,7 @@ void conv3x3_kernel(ConvArgs a) {
       }
       buf = buf + 1 == C::kBuf ? 0 : buf + 1;
     }
-    // the trailing loads (zero fills of unused buffers) land before LDS is reused
+    // every wave is done reading the ring before LDS is reused
     wait_vmcnt_barrier<0>();
 
     // ---- split-K reduction through LDS ----------------------------------
@@ -526,14 +575,16 @@ int launch_cfg(const ConvArgs& a, hipStream_t stream) {
   return launch_status();
 }
 
-constexpr int kNumTiles = 19;
+constexpr int kNumTiles = 25;
 struct TileShape { int bm, bn; };
 //                                   0          1         2          3         4        5
 constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 128}, {32, 32}, {32, 128},
 //   6         7         8          9           10         11          12         13
     {32, 32}, {32, 64}, {32, 128}, {128, 128}, {128, 64}, {128, 128}, {128, 64}, {32, 64},
-//   14          15          16         17         18
-    {256, 128}, {128, 128}, {64, 128}, {128, 64}, {32, 128}};
+//   14          15          16         17         18          19          20          21
+    {256, 128}, {128, 128}, {64, 128}, {128, 64}, {32, 128}, {256, 128}, {128, 256}, {256, 256},
+//   22         23          24
+    {256, 64}, {128, 128}, {128, 128}};
 
 // Tile shape by problem size (rows = output rows of one 4-step chunk, K =
 // 9*Cin or the Linear depth): big tiles while M fills 256 CUs, split-K wave
@@ -641,11 +692,27 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
     case 16: return launch_cfg<2, 2, 1, 2, 1, 4, POOL, MODE, TAPS>(a, s);  // 64 x 128, 96 KB
     case 17: return launch_cfg<4, 1, 1, 2, 1, 5, POOL, MODE, TAPS>(a, s);  // 128 x 64, 120 KB
     case 18: return launch_cfg<1, 2, 1, 2, 2, 3, POOL, MODE, TAPS>(a, s);  // 32 x 128 split-K 2, 120 KB
+    // four-wave and two-wave blocks with 128 x 64 / 64 x 128 / 128 x 128 per
+    // wave: fewer LDS fragment reads per MFMA than the 64 x 64 waves
+    case 19: return launch_cfg<2, 2, 4, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 256 x 128, 144 KB
+    case 20: return launch_cfg<2, 2, 2, 4, 1, 3, POOL, MODE, TAPS>(a, s);  // 128 x 256, 144 KB
+    case 21: return launch_cfg<2, 2, 4, 4, 1, 2, POOL, MODE, TAPS>(a, s);  // 256 x 256, 128 KB
+    case 22: return launch_cfg<2, 1, 4, 2, 1, 2, POOL, MODE, TAPS>(a, s);  // 256 x 64, 80 KB
+    case 23: return launch_cfg<1, 2, 4, 2, 1, 2, POOL, MODE, TAPS>(a, s);  // 128 x 128, 64 KB
+    case 24: return launch_cfg<2, 1, 2, 4, 1, 2, POOL, MODE, TAPS>(a, s);  // 128 x 128, 64 KB
     default: return SNNK_EINVAL;
   }
 }
 
 // Validates a conv call and fills ConvArgs (no launch).
+void set_row_divs(ConvArgs* a) {
+  auto div = [](int d) { return make_fastdiv(static_cast<uint32_t>(std::max(d, 1))); };
+  a->div_howo = div(a->Ho * a->Wo);
+  a->div_wo = div(a->Wo);
+  a->div_hw = div(a->H * a->W);
+  a->div_w = div(a->W);
+}
+
 int conv_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_t* spikes_out,
               float* preact_out, int64_t T, int64_t B, int64_t H, int64_t W, int64_t Cin,
               int64_t Cout, int32_t pool, float decay, float in_scale, float v_threshold,
@@ -663,7 +730,7 @@ int conv_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_t*
   const int64_t step_in = B * H * W * Cin;
   const int64_t step_out = B * H * W * Cout;
   // byte offsets into x and w are 32-bit (buffer descriptors)
-  if (T * step_in * 2 > kOOB || T * step_out > (1ll << 40) || Cout * 9 * Cin * 2 > kOOB)
+  if (T * step_in * 2 > kFar || T * step_out > (1ll << 40) || Cout * 9 * Cin * 2 > kFar)
     return SNNK_EUNSUPPORTED;
   if (check_ptrs && (!aligned(x, 16) || !aligned(w, 16))) return SNNK_EALIGN;
   ConvArgs a{};
@@ -676,6 +743,7 @@ int conv_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_t*
   a.n_quads = pool ? a.B * a.Ho * a.Wo : a.B * a.H * a.W / 4;
   a.n_stages = static_cast<int>((9 * Cin + kKS - 1) / kKS);
   a.div_cin = make_fastdiv(static_cast<uint32_t>(Cin));
+  set_row_divs(&a);
   a.x_tstride_b = static_cast<uint32_t>(step_in * 2);
   a.x_bytes = static_cast<uint32_t>(T * step_in * 2);
   a.w_bytes = static_cast<uint32_t>(Cout * 9 * Cin * 2);
@@ -697,7 +765,7 @@ int linear_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_
     if (preact_out == nullptr && spikes_out == nullptr) return SNNK_EINVAL;
   }
   if (K % 32 != 0 || N % 32 != 0 || R % 4 != 0) return SNNK_EUNSUPPORTED;
-  if (T * R * K * 2 > kOOB || N * K * 2 > kOOB || T * R * N > (1ll << 40))
+  if (T * R * K * 2 > kFar || N * K * 2 > kFar || T * R * N > (1ll << 40))
     return SNNK_EUNSUPPORTED;
   if (check_ptrs && (!aligned(x, 16) || !aligned(w, 16))) return SNNK_EALIGN;
   ConvArgs a{};
@@ -708,6 +776,7 @@ int linear_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_
   a.n_quads = static_cast<int>(R / 4);
   a.n_stages = static_cast<int>((K + kKS - 1) / kKS);
   a.div_cin = make_fastdiv(static_cast<uint32_t>(K));
+  set_row_divs(&a);
   a.x_tstride_b = static_cast<uint32_t>(R * K * 2);
   a.x_bytes = static_cast<uint32_t>(T * R * K * 2);
   a.w_bytes = static_cast<uint32_t>(N * K * 2);

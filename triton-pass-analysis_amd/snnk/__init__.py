@@ -11,7 +11,7 @@ from .kernels import __all__ as _kernels_all
 from .nn import (  # noqa: F401
     IFNode, LIFNode, StatefulLIFNode, RateCodedLIFNode, RateCodedIFNode,
     FusedConvNeuron, FusedLinearNeuron, FusedConvBNNeuron, FusedConvBNAddNeuron,
-    FusedAddNeuron, FusedConvBNLIFPool,
+    FusedAddNeuron, FusedConvBNLIFPool, ChunkedForward, run_chunked,
 )
 from .nn.attention import FusedSpikeAttention  # noqa: F401
 from .verify import assert_equivalent, compare_models  # noqa: F401
@@ -20,6 +20,7 @@ from . import passes  # noqa: F401
 __all__ = list(_kernels_all) + [
     "IFNode", "LIFNode", "StatefulLIFNode", "RateCodedLIFNode", "RateCodedIFNode",
     "FusedConvNeuron", "FusedLinearNeuron", "FusedConvBNNeuron", "FusedConvBNAddNeuron",
+    "ChunkedForward", "run_chunked",
     "FusedAddNeuron", "FusedConvBNLIFPool", "FusedSpikeAttention",
     "assert_equivalent", "compare_models",
 ]

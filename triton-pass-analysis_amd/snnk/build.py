@@ -77,6 +77,13 @@ def build(verbose: bool = True) -> pathlib.Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    # a kernel whose launch stub the host pass failed to emit leaves an
+    # undefined symbol that only shows when the library is loaded
+    res = subprocess.run(["nm", "-D", "--undefined-only", str(tmp)], capture_output=True,
+                         text=True)
+    missing = [ln.split()[-1] for ln in res.stdout.splitlines() if "__device_stub__" in ln]
+    if missing:
+        raise RuntimeError(f"libsnnk has undefined kernel stubs: {missing[:3]}")
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"[snnk.build] {len(srcs)} sources -> {LIB_PATH}")

@@ -4,9 +4,10 @@ from .modules import (
     FusedConvNeuron, FusedLinearNeuron, FusedConvBNNeuron, FusedConvBNAddNeuron,
     FusedAddNeuron, FusedConvBNLIFPool,
 )
+from .chunked import ChunkedForward, run_chunked
 
 __all__ = [
     "IFNode", "LIFNode", "StatefulLIFNode", "RateCodedLIFNode", "RateCodedIFNode",
     "FusedConvNeuron", "FusedLinearNeuron", "FusedConvBNNeuron", "FusedConvBNAddNeuron",
-    "FusedAddNeuron", "FusedConvBNLIFPool",
+    "FusedAddNeuron", "FusedConvBNLIFPool", "ChunkedForward", "run_chunked",
 ]
