@@ -32,6 +32,7 @@
 // an NBUF-deep LDS ring filled by direct global->LDS buffer loads; each
 // lane's source offsets are rebuilt only when the stage's tap changes.
 #include <algorithm>
+#include <type_traits>
 
 #include "snnk_common.h"
 
@@ -280,9 +281,12 @@ void conv3x3_kernel(ConvArgs a) {
     bias_n[j] = (a.bias && col_ok[j]) ? a.bias[n] : 0.0f;
   }
 
-  // bias + LIF over the 4 steps of chunk tc (+ 2x2 OR), or the fp32
-  // pre-activations; run by the kg == 0 waves on the full K sum
-  auto epilogue = [&](const f32x16 (&acc)[TM][TN], int tc) {
+  // bias + LIF over the 4 steps of chunk tc (+ 2x2 OR) on the full K sum;
+  // the reset rule is a compile-time branch (kSoft) so that each neuron
+  // update is add, mul, mul, add, compare, select (+ sub when soft)
+  auto lif_epilogue = [&](const f32x16 (&acc)[TM][TN], int tc, auto soft_tag)
+                          __attribute__((always_inline)) {
+    constexpr bool kSoft = decltype(soft_tag)::value;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int quad = quad0 + (wm * TM + i) * 2 + g_lane;
@@ -291,7 +295,46 @@ void conv3x3_kernel(ConvArgs a) {
       for (int j = 0; j < TN; ++j) {
         if (!col_ok[j]) continue;
         const int n = n0 + (wn * TN + j) * 32 + r_lane;
-        if constexpr (MODE == MODE_PREACT) {
+        uint16_t* o = a.out + static_cast<int64_t>(tc) * 4 * a.o_tstride +
+                      static_cast<int64_t>(POOL ? quad : quad * 4) * a.Cout + n;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (tc * 4 + t >= a.T) break;
+          bool any = false;
+          bool sp[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float u = __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]);
+            const float h = __fadd_rn(__fmul_rn(a.decay, v[i][j][q]), __fmul_rn(a.in_scale, u));
+            const bool s = h >= a.vth;
+            if constexpr (kSoft) v[i][j][q] = s ? __fsub_rn(h, a.vth) : h;
+            else v[i][j][q] = s ? a.v_reset : h;
+            sp[q] = s;
+            any = any || s;
+          }
+          if constexpr (POOL) {
+            o[0] = spike_bf16(any);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q * a.Cout] = spike_bf16(sp[q]);
+          }
+          o += a.o_tstride;
+        }
+      }
+    }
+  };
+  // the LIF epilogue, or the fp32 pre-activations; run by the kg == 0 waves
+  // (both lambdas are forced inline: a call would move the accumulators to scratch)
+  auto epilogue = [&](const f32x16 (&acc)[TM][TN], int tc) __attribute__((always_inline)) {
+    if constexpr (MODE == MODE_PREACT) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int quad = quad0 + (wm * TM + i) * 2 + g_lane;
+        if (quad >= a.n_quads) continue;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if (!col_ok[j]) continue;
+          const int n = n0 + (wn * TN + j) * 32 + r_lane;
 #pragma unroll
           for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -302,33 +345,12 @@ void conv3x3_kernel(ConvArgs a) {
                 a.pre[tg * a.o_tstride + p * a.Cout + n] = __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]);
               }
             }
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int tg = tc * 4 + t;
-            if (tg >= a.T) break;
-            bool any = false;
-            bool sp[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float u = __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]);
-              const float h = __fadd_rn(__fmul_rn(a.decay, v[i][j][q]), __fmul_rn(a.in_scale, u));
-              const bool s = h >= a.vth;
-              v[i][j][q] = s ? (a.soft_reset ? __fsub_rn(h, a.vth) : a.v_reset) : h;
-              sp[q] = s;
-              any = any || s;
-            }
-            uint16_t* o = a.out + static_cast<int64_t>(tg) * a.o_tstride;
-            if constexpr (POOL) {
-              o[static_cast<int64_t>(quad) * a.Cout + n] = spike_bf16(any);
-            } else {
-#pragma unroll
-              for (int q = 0; q < 4; ++q)
-                o[(static_cast<int64_t>(quad) * 4 + q) * a.Cout + n] = spike_bf16(sp[q]);
-            }
-          }
         }
       }
+    } else if (a.soft_reset) {
+      lif_epilogue(acc, tc, std::true_type{});
+    } else {
+      lif_epilogue(acc, tc, std::false_type{});
     }
   };
 
@@ -582,7 +604,7 @@ constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 
 //   6         7         8          9           10         11          12         13
     {32, 32}, {32, 64}, {32, 128}, {128, 128}, {128, 64}, {128, 128}, {128, 64}, {32, 64},
 //   14          15          16         17         18          19          20          21
-    {256, 128}, {128, 128}, {64, 128}, {128, 64}, {32, 128}, {256, 128}, {128, 256}, {256, 256},
+    {256, 128}, {128, 128}, {64, 128}, {128, 64}, {32, 128}, {256, 128}, {128, 256}, {128, 256},
 //   22         23          24
     {256, 64}, {128, 128}, {128, 128}};
 
@@ -692,11 +714,12 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
     case 16: return launch_cfg<2, 2, 1, 2, 1, 4, POOL, MODE, TAPS>(a, s);  // 64 x 128, 96 KB
     case 17: return launch_cfg<4, 1, 1, 2, 1, 5, POOL, MODE, TAPS>(a, s);  // 128 x 64, 120 KB
     case 18: return launch_cfg<1, 2, 1, 2, 2, 3, POOL, MODE, TAPS>(a, s);  // 32 x 128 split-K 2, 120 KB
-    // four-wave and two-wave blocks with 128 x 64 / 64 x 128 / 128 x 128 per
-    // wave: fewer LDS fragment reads per MFMA than the 64 x 64 waves
+    // four-wave and two-wave blocks with 128 x 64 / 64 x 128 per wave (fewer
+    // LDS fragment reads per MFMA than the 64 x 64 waves), and the 8-wave
+    // 128 x 256 transpose of 14
     case 19: return launch_cfg<2, 2, 4, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 256 x 128, 144 KB
     case 20: return launch_cfg<2, 2, 2, 4, 1, 3, POOL, MODE, TAPS>(a, s);  // 128 x 256, 144 KB
-    case 21: return launch_cfg<2, 2, 4, 4, 1, 2, POOL, MODE, TAPS>(a, s);  // 256 x 256, 128 KB
+    case 21: return launch_cfg<2, 4, 2, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 128 x 256, 144 KB
     case 22: return launch_cfg<2, 1, 4, 2, 1, 2, POOL, MODE, TAPS>(a, s);  // 256 x 64, 80 KB
     case 23: return launch_cfg<1, 2, 4, 2, 1, 2, POOL, MODE, TAPS>(a, s);  // 128 x 128, 64 KB
     case 24: return launch_cfg<2, 1, 2, 4, 1, 2, POOL, MODE, TAPS>(a, s);  // 128 x 128, 64 KB
