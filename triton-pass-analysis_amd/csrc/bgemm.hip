@@ -5,9 +5,9 @@
 // with A, B packed along k as uint32 words (bit k%32 of word k/32).
 //
 // Each wave owns a (32*TM)x(32*TN) tile of C as TMxTN MFMA 32x32 accumulators
-// and walks K in stages of 4 words (128 bits).  With TM x TN = 4 x 2 two
-// waves fit a SIMD, so one wave's result stores overlap the other's MFMAs.  Packed words are loaded straight into
-// registers one stage ahead; no LDS.  A packed 32-bit word feeds one MFMA
+// and walks K in stages of 4 words (128 bits) staged through an LDS ring.
+// With TM x TN = 2 x 4 two waves fit a SIMD, so one wave's result stores
+// overlap the other's MFMAs.  A packed 32-bit word feeds one MFMA
 // k-step (32 int8 k values): the lane half g (lane/32) builds its 16 operand
 // bytes as the 4 dwords (w >> (4g+s)) & 0x01010101, s = 0..3, i.e. byte b of
 // dword s holds bit 4g+s+8b.  A and B operands use this same bit->k
@@ -32,7 +32,12 @@ constexpr int kStageW = 4;     // packed words per stage
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 constexpr uint32_t kOOB = 0xFFFFFFF0u;        // buffer offset past every operand
 constexpr int kRsrcWord3 = 0x00020000;       // raw buffer, 32-bit data format
-constexpr int kRing = 8;                     // stages in the LDS ring
+// Stages in the LDS ring: 8 for a 128x128 wave tile (32 KB); 6 for the
+// 128x64 tile (18 KB), so that eight such waves -- two per SIMD -- fit a CU.
+template <int TM, int TN>
+constexpr int ring_depth() { return TM * TN >= 16 ? 8 : 6; }
+template <int TM, int TN>
+constexpr int waves_per_simd() { return TM * TN >= 16 ? 1 : 2; }
 
 __device__ __forceinline__ i32x4 expand(uint32_t w, int g) {
   const uint32_t x = w >> (4 * g);
@@ -73,11 +78,13 @@ __device__ __forceinline__ void mfma_stage(i32x16 (&acc)[TM][TN], const u32x4 (&
 // past M / N read as zeros (range-checked offsets); in the last stage words
 // past KW are cleared and the bits past K of the last word masked.
 template <bool SIGNED, bool OUT_F32, int TM, int TN>
-__global__ __launch_bounds__(64) void bgemm_mfma_kernel(
+__global__ __launch_bounds__(64)
+__attribute__((amdgpu_waves_per_eu(waves_per_simd<TM, TN>()))) void bgemm_mfma_kernel(
     const uint32_t* __restrict__ A, const uint32_t* __restrict__ B, void* __restrict__ Cv,
     int64_t M, int64_t N, int64_t KW, uint32_t last_mask, int64_t lda, int64_t ldb,
     int64_t ldc, int64_t sA, int64_t sB, int64_t sC, uint32_t a_bytes, uint32_t b_bytes) {
   constexpr int kRows = 32 * (TM + TN);          // rows per stage, A then B
+  constexpr int kRing = ring_depth<TM, TN>();
   __shared__ __attribute__((aligned(1024))) u32x4 ring[kRing][kRows];
   const int lane = threadIdx.x;
   const int r32 = lane & 31, g = lane >> 5;
@@ -191,7 +198,10 @@ __global__ __launch_bounds__(64) void bgemm_mfma_kernel(
   }
 }
 
-template <bool SIGNED, bool OUT_F32, int TM = 4, int TN = 4>
+// 64x128 wave tiles, two waves per SIMD: 8192x4096x4096 in 111 us against
+// 121 us for one 128x128 wave per SIMD (its int32 stores could not overlap
+// MFMA work) and 122 us for 128x64.
+template <bool SIGNED, bool OUT_F32, int TM = 2, int TN = 4>
 int launch_mfma(const uint32_t* A, const uint32_t* B, void* C, int64_t batch, int64_t M,
                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t sA,
                 int64_t sB, int64_t sC, hipStream_t stream) {
