@@ -224,6 +224,21 @@ int64_t snnk_linear_bias_lif_ws_size(int64_t T, int64_t R, int64_t K, int64_t N,
                                      int32_t preact, int32_t tile_hint, int32_t splits);
 
 /*
+ * Classifier head averaged over time: out[r][n] = (1/T) * sum_t
+ * (x[t][r] . w[n] + bias[n]), fp32 out [R][N]; same operands, tiling and
+ * workspace contract as snnk_linear_bias_lif_ws (size it with
+ * snnk_linear_bias_lif_ws_size(..., preact = 1, ...)).  Each step's sum is
+ * accumulated in fp32 in step order and divided by T once.
+ *
+ * Replaces the last nn.Linear of the VGG classifier applied per step
+ *   (snn_compiler/zoo/vgg.py:107-114) followed by the caller's mean over T
+ *   (examples/vgg16_snn/benchmark_inference.py:68, `infer_model(xseq).mean(0)`).
+ */
+int snnk_linear_mean_t(const uint16_t* x, const uint16_t* w, const float* bias, float* out,
+                       int64_t T, int64_t R, int64_t K, int64_t N, int32_t tile_hint,
+                       int32_t splits, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Spike self-attention core: per (batch, head) and step t, integer
  * S = Q K^T and O = S V on int8 MFMA over {0,1} spikes (no softmax), then
  * a multi-step LIF on in_scale * O (in_scale = scale / tau for a LIF with

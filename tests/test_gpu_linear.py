@@ -61,3 +61,27 @@ def test_fused_linear_neuron_module_paths():
     near = torch.cummax(((tr - 0.5).abs() < 1e-2).int(), 0).values.bool()
     assert s32.dtype == torch.float32 and not torch.any((s32 != ref) & ~near)
     assert (s16 == ref).float().mean().item() >= 0.999
+
+
+@pytest.mark.parametrize("T,R,K,N,splits", [(4, 32, 4096, 32, 0), (6, 8, 512, 64, 1),
+                                            (1, 12, 256, 96, 1), (5, 32, 1024, 32, 4)])
+def test_linear_mean_t_matches_f64(T, R, K, N, splits):
+    """snnk_linear_mean_t: the time average of x.w^T + b (the classifier head
+    read as model(x).mean(0)) within fp32 accumulation error of float64,
+    and equal to the mean of linear_preact's own per-step outputs within
+    fp32 rounding of the 1/T average."""
+    from snnk.kernels.linear import linear_mean_t
+    g = torch.Generator().manual_seed(T * 1000 + K)
+    x = (torch.rand(T, R, K, generator=g) < 0.2).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * K ** -0.5).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.1
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    m = linear_mean_t(xd, wd, bd, splits=splits).cpu().double()
+    ref = (x.double() @ w.double().t() + b.double()).mean(0)
+    absref = (x.double() @ w.double().abs().t()).mean(0) + b.double().abs()
+    assert m.shape == (R, N)
+    assert torch.all((m - ref).abs() <= 3e-5 * absref + 1e-6)
+    per_step = linear_preact(xd, wd, bd, splits=splits).cpu().double().mean(0)
+    assert torch.allclose(m, per_step, rtol=1e-6, atol=1e-6)
+    # repeated calls are bit-identical (fixed summation order)
+    assert torch.equal(linear_mean_t(xd, wd, bd, splits=splits).cpu().double(), m)

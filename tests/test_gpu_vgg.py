@@ -112,6 +112,21 @@ def test_graph_replay_equals_eager():
         assert not torch.equal(other, eager)
 
 
+def test_mean_over_t_head_and_graph():
+    """forward(mean_t=True) folds the logits' mean over T into the last
+    layer (what the bench times): equal to forward().mean(0) within fp32
+    rounding, eager and replayed."""
+    eng = _engine(3.0)
+    img = _image(32, seed=4).to(DEV)
+    full = eng(img)
+    m = eng(img, mean_t=True)
+    assert m.shape == (32, 10)
+    assert torch.allclose(m, full.mean(0), rtol=1e-6, atol=1e-6)
+    for _ in range(2):
+        eng(_image(32, seed=9).to(DEV))
+        assert torch.equal(eng.run_graph(img, mean_t=True), m)
+
+
 @pytest.mark.parametrize("B", [1, 56])
 def test_batch_curve(B):
     """B=1 pads the FC rows to 4; logits match the oracle (BASELINE init)."""

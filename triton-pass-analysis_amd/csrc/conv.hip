@@ -83,7 +83,9 @@ __device__ __forceinline__ void wait_stages_barrier(int later) {
 __device__ __forceinline__ int swz_key(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
 __device__ __forceinline__ int swz(int r, int c) { return c ^ swz_key(r); }
 
-enum { MODE_LIF = 0, MODE_PREACT = 1 };
+// MODE_MEAN (Linear only): fp32 (x W^T + b) averaged over the T steps,
+// out [R][N], for a classifier head whose logits are read as their mean over T.
+enum { MODE_LIF = 0, MODE_PREACT = 1, MODE_MEAN = 2 };
 
 struct ConvArgs {
   const uint16_t* x;
@@ -345,6 +347,29 @@ void conv3x3_kernel(ConvArgs a) {
                 a.pre[tg * a.o_tstride + p * a.Cout + n] = __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]);
               }
             }
+        }
+      }
+    } else if constexpr (MODE == MODE_MEAN) {
+      // running sum over the steps in v (one chunk of 4 at a time), written
+      // as sum / T after the last chunk
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int quad = quad0 + (wm * TM + i) * 2 + g_lane;
+        if (quad >= a.n_quads) continue;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if (!col_ok[j]) continue;
+          const int n = n0 + (wn * TN + j) * 32 + r_lane;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (tc * 4 + t < a.T)
+                v[i][j][q] = __fadd_rn(v[i][j][q], __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]));
+            if (tc == n_chunks - 1)
+              a.pre[(static_cast<int64_t>(quad) * 4 + q) * a.Cout + n] =
+                  __fdiv_rn(v[i][j][q], static_cast<float>(a.T));
+          }
         }
       }
     } else if (a.soft_reset) {
@@ -816,13 +841,16 @@ int linear_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_
 
 template <int TAPS>
 int run(const ConvArgs& a, bool pool, int tile_hint, int splits, bool allow_split, void* ws,
-        int64_t ws_bytes, hipStream_t s) {
+        int64_t ws_bytes, hipStream_t s, bool mean = false) {
   if (a.T == 0 || a.n_quads == 0) return SNNK_OK;
   Plan p;
   int st = make_plan(a, tile_hint, splits, allow_split, &p);
   if (st != SNNK_OK) return st;
   if (p.ws_bytes > 0 && (ws == nullptr || ws_bytes < p.ws_bytes)) return SNNK_EWORKSPACE;
   if (p.ws_bytes > 0 && !aligned(ws, 256)) return SNNK_EALIGN;
+  if constexpr (TAPS == 1) {
+    if (mean) return dispatch<false, MODE_MEAN, 1>(a, p, ws, s);
+  }
   if (a.pre != nullptr) return dispatch<false, MODE_PREACT, TAPS>(a, p, ws, s);
   if (pool) return dispatch<true, MODE_LIF, TAPS>(a, p, ws, s);
   return dispatch<false, MODE_LIF, TAPS>(a, p, ws, s);
@@ -906,6 +934,19 @@ extern "C" int snnk_linear_bias_lif_ws(const uint16_t* x, const uint16_t* w, con
   if (st != SNNK_OK) return st;
   return run<1>(a, false, tile_hint, splits, true, workspace, workspace_bytes,
                 static_cast<hipStream_t>(stream));
+}
+
+extern "C" int snnk_linear_mean_t(const uint16_t* x, const uint16_t* w, const float* bias,
+                                  float* out, int64_t T, int64_t R, int64_t K, int64_t N,
+                                  int32_t tile_hint, int32_t splits, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  if (T == 0 || R == 0) return (T < 0 || R < 0) ? SNNK_EINVAL : SNNK_OK;
+  if (out == nullptr) return SNNK_EINVAL;
+  ConvArgs a;
+  int st = linear_args(x, w, bias, nullptr, out, T, R, K, N, 0.f, 0.f, 0.f, 0.f, 0, true, &a);
+  if (st != SNNK_OK) return st;
+  return run<1>(a, false, tile_hint, splits, true, workspace, workspace_bytes,
+                static_cast<hipStream_t>(stream), true);
 }
 
 extern "C" int64_t snnk_linear_bias_lif_ws_size(int64_t T, int64_t R, int64_t K, int64_t N,

@@ -94,6 +94,13 @@ PROTOTYPES: dict[str, list] = {
         _i32, _p, _i64,        # splits, workspace, workspace_bytes
         _p,                    # stream
     ],
+    "snnk_linear_mean_t": [
+        _p, _p, _p, _p,        # x, w, bias, out
+        _i64, _i64, _i64, _i64,  # T, R, K, N
+        _i32, _i32,            # tile_hint, splits
+        _p, _i64,              # workspace, workspace_bytes
+        _p,                    # stream
+    ],
     "snnk_spike_attention": [
         _p, _p, _p,            # q, k, v
         _i64, _i64, _i64,      # q_row, k_row, v_row

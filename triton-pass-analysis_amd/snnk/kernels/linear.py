@@ -79,3 +79,29 @@ def linear_preact(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *
         assert out.shape == (T, R, N) and out.dtype == torch.float32 and out.is_contiguous()
     _linear_call(x, w, bias, None, out, 1.0, 1.0, 1.0, 0.0, False, tile_hint, splits)
     return out
+
+
+def linear_mean_t(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
+                  out: torch.Tensor | None = None, tile_hint: int = -1,
+                  splits: int | None = None) -> torch.Tensor:
+    """x [T, R, K] bf16, w [N, K] bf16 -> fp32 mean over T of x.w^T + bias, [R, N].
+
+    A classifier head read as its time average (the reference's
+    ``model(x_seq).mean(0)``, examples/vgg16_snn/benchmark_inference.py:68)
+    in one kernel: the per-step sums stay in registers and only [R, N] is
+    written."""
+    _check(x, w, bias)
+    T, R, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty(R, N, device=x.device, dtype=torch.float32)
+    else:
+        assert out.shape == (R, N) and out.dtype == torch.float32 and out.is_contiguous()
+    sp = 0 if splits is None else int(splits)
+    with torch.cuda.device(x.device):
+        nbytes = _abi.size_call("snnk_linear_bias_lif_ws_size", T, R, K, N, 1, int(tile_hint), sp)
+        ws = _workspace.get(x.device, nbytes)
+        _abi.call("snnk_linear_mean_t", x.data_ptr(), w.data_ptr(), _abi.ptr(bias), out.data_ptr(),
+                  T, R, K, N, int(tile_hint), sp, _abi.ptr(ws), 0 if ws is None else ws.numel(),
+                  _abi.stream(x.device))
+    return out

@@ -30,7 +30,7 @@ from ..nn.modules import (
 from ..passes.fuse import fuse_snn_model
 from ..kernels.conv import conv3x3_image_lif
 from ..kernels.fused import fold_conv_bn
-from ..kernels.linear import linear_bias_lif, linear_preact
+from ..kernels.linear import linear_bias_lif, linear_preact, linear_mean_t
 from ..kernels.neurons import neuron_params
 
 VGG16_CFG = [64, 64, "P", 128, 128, "P", 256, 256, 256, "P",
@@ -258,9 +258,13 @@ class FusedVGGSNN(nn.Module):
                 rates.append(x.float().mean())
         return x
 
-    def forward(self, image: torch.Tensor, rates: list | None = None) -> torch.Tensor:
+    def forward(self, image: torch.Tensor, rates: list | None = None,
+                mean_t: bool = False) -> torch.Tensor:
         """image [B, 3, H, W] (static, shown at all T steps) or [T, B, 3, H, W]
-        with identical steps -> logits [T, B, num_classes] fp32."""
+        with identical steps -> logits [T, B, num_classes] fp32, or with
+        ``mean_t`` their mean over T, [B, num_classes], computed in the last
+        layer's kernel (the reference's inference reads ``model(x).mean(0)``,
+        examples/vgg16_snn/benchmark_inference.py:68)."""
         if image.ndim == 5:
             assert image.shape[0] == self.T, f"expected T={self.T} steps"
             # the engine computes the input layer once for a static image
@@ -280,16 +284,19 @@ class FusedVGGSNN(nn.Module):
         x = linear_bias_lif(x, self.fc2_w, self.fc2_b, **self._lif())
         if rates is not None:
             rates.append(x[:, :B].float().mean())
+        if mean_t:
+            return linear_mean_t(x, self.fc3_w, self.fc3_b)[:B, :self.num_classes]
         y = linear_preact(x, self.fc3_w, self.fc3_b)
         return y[:, :B, :self.num_classes]
 
     @torch.no_grad()
-    def capture(self, B: int, H: int = 32, W: int = 32, device=None, x_in=None):
+    def capture(self, B: int, H: int = 32, W: int = 32, device=None, x_in=None,
+                mean_t: bool = False):
         """Record forward for batch B in a HIP graph; returns (graph, in, out).
 
         ``x_in`` (optional, fp32 contiguous [B, 3, H, W]) becomes the graph's
         input buffer; by default a new one is allocated and the graph is kept
-        for :meth:`run_graph`."""
+        for :meth:`run_graph`.  ``mean_t`` as in :meth:`forward`."""
         device = device or self.w0.device
         keep = x_in is None
         if keep:
@@ -298,21 +305,21 @@ class FusedVGGSNN(nn.Module):
         stream = torch.cuda.Stream(device)
         stream.wait_stream(torch.cuda.current_stream(device))
         with torch.cuda.stream(stream):
-            self.forward(x_in)  # warm-up outside the capture
+            self.forward(x_in, mean_t=mean_t)  # warm-up outside the capture
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream):
-                y = self.forward(x_in)
+                y = self.forward(x_in, mean_t=mean_t)
         torch.cuda.current_stream(device).wait_stream(stream)
         torch.cuda.synchronize(device)
         if keep:
-            self._graphs[(B, H, W)] = (graph, x_in, y)
+            self._graphs[(B, H, W, mean_t)] = (graph, x_in, y)
         return graph, x_in, y
 
     @torch.no_grad()
-    def run_graph(self, image: torch.Tensor) -> torch.Tensor:
-        key = (image.shape[0], image.shape[2], image.shape[3])
+    def run_graph(self, image: torch.Tensor, mean_t: bool = False) -> torch.Tensor:
+        key = (image.shape[0], image.shape[2], image.shape[3], mean_t)
         if key not in self._graphs:
-            self.capture(*key, device=image.device)
+            self.capture(*key[:3], device=image.device, mean_t=mean_t)
         graph, x_in, y = self._graphs[key]
         x_in.copy_(image)
         graph.replay()
