@@ -223,6 +223,7 @@ def bench_lif(args, dev):
 # Bit-packed binary GEMM
 # --------------------------------------------------------------------------
 INT8_PEAK_TOPS = 5030.0
+FP4_PEAK_TOPS = 10100.0  # dense MX fp4 / fp6 MFMA
 
 
 def bench_bgemm(args, dev):
@@ -244,8 +245,10 @@ def bench_bgemm(args, dev):
     Ws = [Wp.clone() for _ in range(nsets)]
     Cs = [torch.empty(M, N, device=dev, dtype=torch.int32) for _ in range(nsets)]
 
+    algo = args.bgemm_algo
+
     def step(i):
-        _gemm_packed(As[i], Ws[i], K, signed=False, algo="mfma", out_dtype=torch.int32,
+        _gemm_packed(As[i], Ws[i], K, signed=False, algo=algo, out_dtype=torch.int32,
                      out=Cs[i])
 
     wall, kern_ms = time_gpu(step, nsets, args.steps, args.warmup)
@@ -256,6 +259,11 @@ def bench_bgemm(args, dev):
     ok = np.array_equal(Cn[:64], clib.popcount_gemm(Ap_ref, Wp_ref, rows=(0, 64)))
     ok = ok and np.array_equal(Cn.sum(1), A_np.astype(np.int64) @ W_np.astype(np.int64).sum(1))
     ok = ok and np.array_equal(Cn.sum(0), A_np.astype(np.int64).sum(0) @ W_np.astype(np.int64))
+    # the other MFMA kernel on the same operands, for comparison
+    other = "mfma" if algo != "mfma" else "mfma_f4"
+    _, other_ms = time_gpu(lambda i: _gemm_packed(As[i], Ws[i], K, signed=False, algo=other,
+                                                  out_dtype=torch.int32, out=Cs[i]),
+                           nsets, args.steps, 2)
 
     # one-off operand packing cost (activations would be packed per call)
     A_u8 = A.to(dev, torch.uint8)
@@ -268,18 +276,29 @@ def bench_bgemm(args, dev):
     torch.cuda.synchronize()
     pack_ms = e0.elapsed_time(e1) / 20
 
+    kinds = {"mfma_f4": ("bgemm_f4_kernel", FP4_PEAK_TOPS,
+                         "dense MX fp4 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4)"),
+             "mfma": ("bgemm_mfma_kernel", INT8_PEAK_TOPS,
+                      "dense int8 MFMA (v_mfma_i32_32x32x32_i8)"),
+             "popc": ("popcount_gemm_kernel", INT8_PEAK_TOPS,
+                      "VALU popcount, priced against the int8 MFMA peak")}
+    kname, peak, note = kinds[algo]
     achieved = ops / (kern_ms * 1e-3) / 1e12
+    other_tops = ops / (other_ms * 1e-3) / 1e12
     rec = {
         "workload": "bgemm", "value": ops / wall / 1e12, "unit": "TOPS",
         "ms_per_step": wall * 1e3, "dtype": "u1 (bit-packed u32) x u1 -> i32",
         "config": {"workload": "binary_gemm_M8192_K4096_N4096_packed_u32", "M": M, "K": K,
-                   "N": N, "p_A": 0.1, "p_W": 0.5, "signed": False, "algo": "mfma_i8",
+                   "N": N, "p_A": 0.1, "p_W": 0.5, "signed": False, "algo": algo,
                    "rotating_sets": nsets},
-        "roofline": {"bound": "mfma", "kernel": "bgemm_mfma_kernel",
-                     "achieved": achieved, "peak": INT8_PEAK_TOPS, "unit": "TOPS",
-                     "frac": achieved / INT8_PEAK_TOPS, "traffic": None,
+        "roofline": {"bound": "mfma", "kernel": kname,
+                     "achieved": achieved, "peak": peak, "unit": "TOPS",
+                     "frac": achieved / peak, "traffic": None,
                      "algorithmic_ops": ops, "kernel_ms_mean": kern_ms,
-                     "peak_note": "dense int8 MFMA (v_mfma_i32_32x32x32_i8)"},
+                     "peak_note": note},
+        "compare": {"algo": other, "kernel": kinds[other][0], "kernel_ms_mean": other_ms,
+                    "achieved": other_tops, "peak": kinds[other][1],
+                    "frac": other_tops / kinds[other][1]},
         "pack_A_ms": pack_ms,
         "parity": bool(ok),
     }
@@ -626,6 +645,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="all", choices=["all", *WORKLOADS])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--bgemm-algo", default="mfma_f4", choices=["mfma", "mfma_f4", "popc"],
+                    help="binary GEMM kernel of the bgemm workload")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: every path here runs on a single MI355X "
@@ -657,7 +678,8 @@ def main():
         "cpu_baseline": head.get("cpu_baseline"),
         "parity": head["parity"],
         "components": {n: {k: r[k] for k in ("value", "unit", "ms_per_step", "roofline",
-                                             "parity", "cpu_baseline", "config") if k in r}
+                                             "parity", "cpu_baseline", "config", "compare",
+                                             "variants") if k in r}
                        for n, r in recs.items() if n != names[0]},
     }
     print(json.dumps(out), flush=True)

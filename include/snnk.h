@@ -114,9 +114,10 @@ int snnk_pack_bits(const void* src, int32_t src_dtype, uint32_t* dst,
                    void* stream);
 
 /* binary GEMM algorithms */
-#define SNNK_BGEMM_AUTO    0   /* MFMA when M, N, K >= 128, else POPC          */
+#define SNNK_BGEMM_AUTO    0   /* MFMA_F4 when M, N, K >= 128, else POPC       */
 #define SNNK_BGEMM_POPC    1   /* VALU and + popcount-accumulate               */
 #define SNNK_BGEMM_MFMA_I8 2   /* bits expanded to int8, v_mfma_i32_32x32x32_i8 */
+#define SNNK_BGEMM_MFMA_F4 3   /* bits expanded to e2m1 0/1.0, MX fp4 MFMA      */
 
 /*
  * Batched binary GEMM over bit-packed operands:

@@ -54,7 +54,7 @@ def test_spike_ktv_popcount_bit_exact():
     assert torch.equal(out.cpu(), k.transpose(-2, -1) @ v)
 
 
-@pytest.mark.parametrize("algo", ["popc", "mfma"])
+@pytest.mark.parametrize("algo", ["popc", "mfma", "mfma_f4"])
 @pytest.mark.parametrize("signed", [False, True])
 @pytest.mark.parametrize("M,N,K", [(5, 7, 33), (64, 48, 64), (130, 70, 70), (300, 257, 1000),
                                    (256, 256, 4096), (129, 384, 128)])
@@ -66,7 +66,7 @@ def test_binary_gemm_small_shapes(algo, signed, M, N, K):
     assert C.dtype == torch.int32 and np.array_equal(C.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("algo", ["popc", "mfma"])
+@pytest.mark.parametrize("algo", ["popc", "mfma", "mfma_f4"])
 def test_binary_gemm_batched_and_float_out(algo):
     A = _bern((3, 200, 150), 0.2, 9)
     W = _bern((3, 150, 140), 0.5, 10)
@@ -86,7 +86,7 @@ def test_garbage_bits_past_K_are_ignored():
     Ap[:, 1] |= torch.tensor(-256, dtype=torch.int32, device=DEV)   # set bits 8..31 (k >= 40)
     Wp[:, 1] |= torch.tensor(-256, dtype=torch.int32, device=DEV)
     ref = ob.binary_gemm_closed_form(A.numpy(), W.numpy())
-    for algo in ("popc", "mfma"):
+    for algo in ("popc", "mfma", "mfma_f4"):
         C = snnk.binary_gemm(Ap, Wp, a_packed=True, w_packed=True, K=40, algo=algo)
         assert np.array_equal(C.cpu().numpy(), ref)
 
@@ -108,6 +108,9 @@ def test_binary_gemm_baseline_config(signed):
     C_popc = snnk.binary_gemm(Ap, Wp, a_packed=True, w_packed=True, K=K, signed=signed,
                               algo="popc")
     assert torch.equal(C, C_popc)
+    C_f4 = snnk.binary_gemm(Ap, Wp, a_packed=True, w_packed=True, K=K, signed=signed,
+                            algo="mfma_f4")
+    assert torch.equal(C_f4, C_popc)
     Cn = C.cpu().numpy().astype(np.int64)
     # exact row sample (first, middle and last rows) against the C oracle
     for m0 in (0, 4064, M - 32):

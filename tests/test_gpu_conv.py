@@ -60,7 +60,8 @@ SHAPES = [  # T, B, Cin, Cout, H, W, tile
     (5, 2, 64, 96, 8, 8, 15), (4, 2, 32, 128, 4, 6, 16), (6, 2, 64, 64, 8, 8, 17),
     (4, 1, 128, 160, 4, 4, 18), (4, 3, 64, 128, 10, 6, 19), (5, 2, 64, 96, 8, 8, 20),
     (2, 2, 64, 256, 8, 8, 21), (3, 2, 96, 256, 6, 6, 21), (4, 3, 32, 64, 10, 6, 22), (4, 2, 64, 160, 8, 8, 23),
-    (3, 2, 64, 128, 6, 6, 24),
+    (3, 2, 64, 128, 6, 6, 24), (4, 2, 64, 96, 4, 4, 25), (3, 2, 96, 128, 6, 6, 26),
+    (5, 2, 64, 128, 8, 8, 27), (4, 1, 128, 160, 4, 4, 28),
 ]
 
 

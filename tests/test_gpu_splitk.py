@@ -42,7 +42,7 @@ def _conv_operands(T, B, H, W, Cin, Cout, seed):
 @pytest.mark.parametrize("T,B,H,W,Cin,Cout,tile,splits", [
     (4, 32, 4, 4, 512, 512, 2, 4), (4, 32, 2, 2, 512, 512, 2, 8), (4, 32, 4, 4, 256, 512, 10, 3),
     (6, 8, 4, 4, 256, 256, 3, 5), (4, 8, 2, 2, 512, 512, -1, 0), (4, 4, 4, 4, 128, 96, 8, 2),
-    (3, 8, 4, 4, 64, 64, 6, 2),
+    (3, 8, 4, 4, 64, 64, 6, 2), (4, 32, 2, 2, 512, 512, 25, 2), (4, 32, 4, 4, 512, 512, 27, 3),
 ])
 def test_conv_split_preact_matches_f64(T, B, H, W, Cin, Cout, tile, splits):
     xd, wp, bd, ref, absref = _conv_operands(T, B, H, W, Cin, Cout, seed=Cin + Cout + splits)

@@ -274,14 +274,10 @@ void conv3x3_kernel(ConvArgs a) {
       for (int q = 0; q < 4; ++q) v[i][j][q] = 0.0f;
 
   const int g_lane = lane >> 5, r_lane = lane & 31;
+  // epilogue columns and bias, filled after the first operand loads are on
+  // their way (the code before them runs once, from a cold instruction cache)
   float bias_n[TN];
   bool col_ok[TN];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = n0 + (wn * TN + j) * 32 + r_lane;
-    col_ok[j] = n < a.Cout;
-    bias_n[j] = (a.bias && col_ok[j]) ? a.bias[n] : 0.0f;
-  }
 
   // bias + LIF over the 4 steps of chunk tc (+ 2x2 OR) on the full K sum;
   // the reset rule is a compile-time branch (kSoft) so that each neuron
@@ -380,14 +376,6 @@ void conv3x3_kernel(ConvArgs a) {
   };
 
   for (int tc = 0; tc < n_chunks; ++tc) {
-    f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
     // Source offsets of this lane's A segments for the tap pair (tap_lo,
     // tap_hi) of the stage last prepared: kFar where the row, the step or
     // the tap's source pixel does not exist.  A stage then costs one add
@@ -472,6 +460,22 @@ void conv3x3_kernel(ConvArgs a) {
 #pragma unroll
       for (int i = 0; i < C::kSegPer; ++i) issue_seg(sp, i, p);
     }
+    // set-up that no load waits for
+    if (tc == 0) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + (wn * TN + j) * 32 + r_lane;
+        col_ok[j] = n < a.Cout;
+        bias_n[j] = (a.bias && col_ok[j]) ? a.bias[n] : 0.0f;
+      }
+    }
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
     constexpr int kSlices = kKS / 16;
     int buf = 0;
     // addressing of the stage the next iteration loads; prepared at the end
@@ -626,7 +630,7 @@ int launch_cfg(const ConvArgs& a, hipStream_t stream) {
   return launch_status();
 }
 
-constexpr int kNumTiles = 25;
+constexpr int kNumTiles = 29;
 struct TileShape { int bm, bn; };
 //                                   0          1         2          3         4        5
 constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 128}, {32, 32}, {32, 128},
@@ -634,8 +638,8 @@ constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 
     {32, 32}, {32, 64}, {32, 128}, {128, 128}, {128, 64}, {128, 128}, {128, 64}, {32, 64},
 //   14          15          16         17         18          19          20          21
     {256, 128}, {128, 128}, {64, 128}, {128, 64}, {32, 128}, {256, 128}, {128, 256}, {128, 256},
-//   22         23          24
-    {256, 64}, {128, 128}, {128, 128}};
+//   22         23          24          25        26        27         28
+    {256, 64}, {128, 128}, {128, 128}, {32, 32}, {32, 64}, {64, 128}, {32, 128}};
 
 // Tile shape by problem size (rows = output rows of one 4-step chunk, K =
 // 9*Cin or the Linear depth): big tiles while M fills 256 CUs, split-K wave
@@ -752,6 +756,12 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
     case 22: return launch_cfg<2, 1, 4, 2, 1, 2, POOL, MODE, TAPS>(a, s);  // 256 x 64, 80 KB
     case 23: return launch_cfg<1, 2, 4, 2, 1, 2, POOL, MODE, TAPS>(a, s);  // 128 x 128, 64 KB
     case 24: return launch_cfg<2, 1, 2, 4, 1, 2, POOL, MODE, TAPS>(a, s);  // 128 x 128, 64 KB
+    // deeper rings (4-5 stages) for the layers that stream their weights
+    // from memory: more stages in flight per block hide the longer latency
+    case 25: return launch_cfg<1, 1, 1, 1, 4, 5, POOL, MODE, TAPS>(a, s);  // 32 x 32 split-K 4, 160 KB
+    case 26: return launch_cfg<1, 1, 1, 2, 2, 5, POOL, MODE, TAPS>(a, s);  // 32 x 64 split-K 2, 120 KB
+    case 27: return launch_cfg<2, 2, 1, 2, 1, 5, POOL, MODE, TAPS>(a, s);  // 64 x 128, 120 KB
+    case 28: return launch_cfg<1, 2, 1, 2, 2, 4, POOL, MODE, TAPS>(a, s);  // 32 x 128 split-K 2, 160 KB
     default: return SNNK_EINVAL;
   }
 }

@@ -25,7 +25,7 @@ SPIKE_SAME, SPIKE_U8, SPIKE_BF16, SPIKE_BITS = 0, 1, 2, 3
 # threshold modes
 THR_SCALAR, THR_PER_CHANNEL, THR_PER_NEURON = 0, 1, 2
 # binary GEMM algorithms
-BGEMM_AUTO, BGEMM_POPC, BGEMM_MFMA_I8 = 0, 1, 2
+BGEMM_AUTO, BGEMM_POPC, BGEMM_MFMA_I8, BGEMM_MFMA_F4 = 0, 1, 2, 3
 
 _p = C.c_void_p
 _i32 = C.c_int32

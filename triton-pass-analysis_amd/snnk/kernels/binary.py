@@ -4,7 +4,7 @@
 (snn_compiler/kernels/attention.py:195-214,236-242; bit n%32 of word n//32,
 LSB first, int32 words).  ``binary_gemm`` generalises its popcount K^T V
 (snn_compiler/kernels/attention.py:217-233,245-258) to any [M,K] x [K,N]
-binary product, with an int8-MFMA algorithm for large shapes and the signed
+binary product, with int8- and fp4-MFMA algorithms for large shapes and the signed
 {-1,+1}-weight form ``2*popc(A & W+) - popc(A)``.
 """
 from __future__ import annotations
@@ -15,7 +15,8 @@ import torch
 
 from .. import _abi
 
-_ALGOS = {"auto": _abi.BGEMM_AUTO, "popc": _abi.BGEMM_POPC, "mfma": _abi.BGEMM_MFMA_I8}
+_ALGOS = {"auto": _abi.BGEMM_AUTO, "popc": _abi.BGEMM_POPC, "mfma": _abi.BGEMM_MFMA_I8,
+          "mfma_f4": _abi.BGEMM_MFMA_F4}
 
 
 def packed_words(K: int) -> int:
@@ -86,7 +87,8 @@ def binary_gemm(A, W, *, signed: bool = False, a_packed: bool = False,
        output column packed along K) with ``w_packed=True``.
     signed: weights are -1 where W is 0 and +1 where W is 1:
        ``C = 2*popc(A & W) - popc(A)``.
-    algo: 'auto' | 'popc' (VALU popcount) | 'mfma' (int8 MFMA).
+    algo: 'auto' | 'popc' (VALU popcount) | 'mfma' (int8 MFMA) | 'mfma_f4'
+       (MX fp4 MFMA, bits as e2m1 0/1.0, exact fp32 counts).
     out: optional preallocated contiguous result tensor.
     """
     if algo not in _ALGOS:
