@@ -15,70 +15,130 @@
 namespace snnk {
 namespace {
 
-// One thread per output pixel and group of 8 output channels, channel group
-// fastest: the lanes of one pixel share its image reads (broadcast) and a
-// wave's spike stores are contiguous 16-byte runs.  The folded weights of all
-// output channels sit in LDS as [cin*9 + tap][Cout].
+// One thread per run of kImgP consecutive output pixels along x and group
+// of 8 output channels, channel group fastest: the 8 lanes of a pixel run
+// share its image reads (broadcast), each weight read from LDS feeds kImgP
+// FMAs, and a spike store of 8 lanes is one full 128-byte line.  The folded
+// weights of all output channels sit in LDS as [cin*9 + tap][Cout], staged
+// with every global read of a thread issued before its LDS writes (the
+// reads follow w's [Cout][K] order, so they coalesce).  Input channels go in
+// chunks of CC: a chunk's image reads (3 rows x (P+2) columns per channel)
+// are all issued before its FMAs, the first chunk's while the block stages
+// the weights.  Runs of P = 4 pixels need W % 4 == 0 and a grid that still
+// fills the GPU; otherwise runs are single pixels.
 constexpr int kImgG = 8;
 constexpr int kImgMaxLds = 64 * 1024;
 
+template <int P, int CC>
 __global__ __launch_bounds__(256) void conv_image_lif_kernel(
     const float* __restrict__ img, const float* __restrict__ w, const float* __restrict__ bias,
     uint16_t* __restrict__ out, int T, int n_pix, int Cin, int H, int W, int Cout, float decay,
     float in_scale, float vth, float v_reset, int soft_reset) {
   extern __shared__ float wl[];
   const int K = Cin * 9;
-  for (int i = threadIdx.x; i < K * Cout; i += 256) {
-    const int k = i / Cout, n = i - k * Cout;
-    wl[i] = w[static_cast<int64_t>(n) * K + k];
-  }
-  __syncthreads();
   const int groups = Cout / kImgG;
+  const int n_runs = n_pix / P;
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (gid >= static_cast<int64_t>(n_pix) * groups) return;
-  const int p = static_cast<int>(gid / groups);  // (b, y, x)
-  const int n0 = (static_cast<int>(gid) - p * groups) * kImgG;
+  const bool live = gid < static_cast<int64_t>(n_runs) * groups;
+  const int g0 = live ? static_cast<int>(gid) : 0;  // threads past the end stage weights only
+  const int run = g0 / groups;
+  const int p = run * P;  // first pixel (b, y, x) of the run
+  const int n0 = (g0 - run * groups) * kImgG;
   const int HW = H * W;
   const int b = p / HW;
   const int r = p - b * HW;
   const int y = r / W, x = r - y * W;
 
-  float acc[kImgG];
+  // image taps of one channel chunk: rows y-1..y+1, columns x-1..x+P
+  // (zero outside the image or past Cin)
+  float xin[CC][3][P + 2];
+  auto load_chunk = [&](int c0) {
 #pragma unroll
-  for (int j = 0; j < kImgG; ++j) acc[j] = 0.0f;
-  for (int c = 0; c < Cin; ++c) {
-    const float* ip = img + (static_cast<int64_t>(b) * Cin + c) * HW;
+    for (int cc = 0; cc < CC; ++cc) {
+      const int c = c0 + cc;
+      const float* ip = img + (static_cast<int64_t>(b) * Cin + (c < Cin ? c : 0)) * HW;
 #pragma unroll
-    for (int tap = 0; tap < 9; ++tap) {
-      const int ys = y + tap / 3 - 1, xs = x + tap % 3 - 1;
-      const float v = (ys >= 0 && ys < H && xs >= 0 && xs < W) ? ip[ys * W + xs] : 0.0f;
-      const float* wk = wl + (c * 9 + tap) * Cout + n0;
+      for (int dy = 0; dy < 3; ++dy)
 #pragma unroll
-      for (int j = 0; j < kImgG; ++j) acc[j] = __builtin_fmaf(v, wk[j], acc[j]);
+        for (int dx = 0; dx < P + 2; ++dx) {
+          const int ys = y + dy - 1, xs = x + dx - 1;
+          const bool in = live && c < Cin && ys >= 0 && ys < H && xs >= 0 && xs < W;
+          xin[cc][dy][dx] = in ? ip[ys * W + xs] : 0.0f;
+        }
+    }
+  };
+  load_chunk(0);
+  constexpr int kStageU = 8;
+  for (int i0 = 0; i0 < K * Cout; i0 += 256 * kStageU) {
+    float tmp[kStageU];
+#pragma unroll
+    for (int u = 0; u < kStageU; ++u) {
+      const int i = i0 + u * 256 + threadIdx.x;
+      tmp[u] = i < K * Cout ? w[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kStageU; ++u) {
+      const int i = i0 + u * 256 + threadIdx.x;
+      if (i < K * Cout) {
+        const int n = i / K, k = i - n * K;
+        wl[k * Cout + n] = tmp[u];
+      }
     }
   }
-  if (bias) {
-#pragma unroll
-    for (int j = 0; j < kImgG; ++j) acc[j] += bias[n0 + j];
-  }
+  __syncthreads();
+  if (!live) return;
 
-  float v[kImgG];
+  float acc[P][kImgG];
 #pragma unroll
-  for (int j = 0; j < kImgG; ++j) v[j] = 0.0f;
+  for (int q = 0; q < P; ++q)
+#pragma unroll
+    for (int j = 0; j < kImgG; ++j) acc[q][j] = 0.0f;
+  for (int c0 = 0; c0 < Cin; c0 += CC) {
+    if (c0 > 0) load_chunk(c0);
+#pragma unroll
+    for (int cc = 0; cc < CC; ++cc) {
+      if (c0 + cc >= Cin) break;
+#pragma unroll
+      for (int tap = 0; tap < 9; ++tap) {
+        const float* wk = wl + ((c0 + cc) * 9 + tap) * Cout + n0;
+        float wv[kImgG];
+#pragma unroll
+        for (int j = 0; j < kImgG; ++j) wv[j] = wk[j];
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+#pragma unroll
+          for (int j = 0; j < kImgG; ++j)
+            acc[q][j] = __builtin_fmaf(xin[cc][tap / 3][tap % 3 + q], wv[j], acc[q][j]);
+      }
+    }
+  }
+  float bv[kImgG];
+#pragma unroll
+  for (int j = 0; j < kImgG; ++j) bv[j] = bias ? bias[n0 + j] : 0.0f;
+
   const int64_t step = static_cast<int64_t>(n_pix) * Cout;
-  uint16_t* o = out + static_cast<int64_t>(p) * Cout + n0;
-  for (int t = 0; t < T; ++t) {
-    uint32_t bits[kImgG / 2];
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    float u[kImgG], v[kImgG];
 #pragma unroll
     for (int j = 0; j < kImgG; ++j) {
-      const float h = __fadd_rn(__fmul_rn(decay, v[j]), __fmul_rn(in_scale, acc[j]));
-      const bool s = h >= vth;
-      v[j] = s ? (soft_reset ? __fsub_rn(h, vth) : v_reset) : h;
-      const uint32_t sb = s ? 0x3F80u : 0u;
-      if (j & 1) bits[j / 2] |= sb << 16;
-      else bits[j / 2] = sb;
+      u[j] = bias ? acc[q][j] + bv[j] : acc[q][j];
+      v[j] = 0.0f;
     }
-    *reinterpret_cast<u32x4*>(o + t * step) = u32x4{bits[0], bits[1], bits[2], bits[3]};
+    uint16_t* o = out + static_cast<int64_t>(p + q) * Cout + n0;
+    for (int t = 0; t < T; ++t) {
+      uint32_t bits[kImgG / 2];
+#pragma unroll
+      for (int j = 0; j < kImgG; ++j) {
+        const float h = __fadd_rn(__fmul_rn(decay, v[j]), __fmul_rn(in_scale, u[j]));
+        const bool s = h >= vth;
+        v[j] = s ? (soft_reset ? __fsub_rn(h, vth) : v_reset) : h;
+        const uint32_t sb = s ? 0x3F80u : 0u;
+        if (j & 1) bits[j / 2] |= sb << 16;
+        else bits[j / 2] = sb;
+      }
+      *reinterpret_cast<u32x4*>(o + t * step) = u32x4{bits[0], bits[1], bits[2], bits[3]};
+    }
   }
 }
 
@@ -144,9 +204,15 @@ extern "C" int snnk_conv3x3_image_lif(const float* image, const float* w, const 
     return SNNK_EUNSUPPORTED;
   if (!aligned(spikes_out, 16)) return SNNK_EALIGN;
   const int64_t n_pix = B * H * W;
-  const int64_t blocks = (n_pix * (Cout / kImgG) + 255) / 256;
+  // runs of 4 pixels per thread when that still gives every CU a block
+  const int run = (W % 4 == 0 && n_pix / 4 * (Cout / kImgG) >= 256 * 256) ? 4 : 1;
+  const int64_t blocks = (n_pix / run * (Cout / kImgG) + 255) / 256;
   if (blocks > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
-  hipLaunchKernelGGL(conv_image_lif_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256),
+  // channel chunk: 3 for RGB-like inputs, else 4
+  const bool c3 = Cin % 3 == 0;
+  auto kern = run == 4 ? (c3 ? conv_image_lif_kernel<4, 3> : conv_image_lif_kernel<4, 4>)
+                       : (c3 ? conv_image_lif_kernel<1, 3> : conv_image_lif_kernel<1, 4>);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256),
                      static_cast<unsigned>(lds), static_cast<hipStream_t>(stream), image, w,
                      bias, spikes_out, static_cast<int>(T), static_cast<int>(n_pix),
                      static_cast<int>(Cin), static_cast<int>(H), static_cast<int>(W),
