@@ -225,6 +225,26 @@ int64_t snnk_linear_bias_lif_ws_size(int64_t T, int64_t R, int64_t K, int64_t N,
                                      int32_t preact, int32_t tile_hint, int32_t splits);
 
 /*
+ * snnk_linear_bias_lif_ws followed by an OR over each group of four adjacent
+ * output columns: spikes_out [T][R][N/4] bf16, column c = max of the spikes of
+ * columns 4c..4c+3 (the LIF runs per column first).  Same operands,
+ * tiling and workspace contract (size it with snnk_linear_bias_lif_ws_size,
+ * preact = 0).
+ *
+ * Replaces, for a 2x2 feature map, conv3x3 + BN + LIF + 2x2 max-pool
+ *   (snn_compiler/nn/modules.py:324-357, snn_compiler/zoo/vgg.py:101-105):
+ *   with every output pixel seeing all four input pixels, the conv is one
+ *   dense matrix over (pixel, channel) -- w [(cout, pixel_out)][(pixel_in,
+ *   cin)] -- and the pool is the OR over the four pixel columns of a channel.
+ */
+int snnk_linear_bias_lif_pool4_ws(const uint16_t* x, const uint16_t* w, const float* bias,
+                                  uint16_t* spikes_out, int64_t T, int64_t R, int64_t K,
+                                  int64_t N, float decay, float in_scale, float v_threshold,
+                                  float v_reset, int32_t soft_reset, int32_t tile_hint,
+                                  int32_t splits, void* workspace, int64_t workspace_bytes,
+                                  void* stream);
+
+/*
  * Classifier head averaged over time: out[r][n] = (1/T) * sum_t
  * (x[t][r] . w[n] + bias[n]), fp32 out [R][N]; same operands, tiling and
  * workspace contract as snnk_linear_bias_lif_ws (size it with

@@ -85,3 +85,70 @@ def test_linear_mean_t_matches_f64(T, R, K, N, splits):
     assert torch.allclose(m, per_step, rtol=1e-6, atol=1e-6)
     # repeated calls are bit-identical (fixed summation order)
     assert torch.equal(linear_mean_t(xd, wd, bd, splits=splits).cpu().double(), m)
+
+
+@pytest.mark.parametrize("T,R,K,N,splits", [(4, 32, 2048, 2048, 0), (5, 8, 256, 128, 1),
+                                            (3, 12, 512, 256, 2)])
+def test_linear_pool4_epilogue_exact(T, R, K, N, splits):
+    """snnk_linear_bias_lif_pool4_ws: the LIF runs per column and the output is
+    the OR of each group of four adjacent columns; exact against the oracle's
+    LIF + column max applied to the kernel's own pre-activations."""
+    from snnk.kernels.linear import linear_bias_lif_pool4
+    x, w, b = _data(T, R, K, N, seed=K + 7 * N)
+    xd, wd, bd = x.to(DEV, torch.bfloat16), w.to(DEV, torch.bfloat16), b.to(DEV)
+    for soft, vth in ((False, 0.5), (True, 0.25)):
+        s = linear_bias_lif_pool4(xd, wd, bd, decay=0.5, in_scale=0.5, v_threshold=vth,
+                                  soft_reset=soft, splits=splits).cpu().float()
+        pre = linear_preact(xd, wd, bd, splits=splits).cpu()
+        spk, _, _ = on.lif_multistep(pre, neuron="lif", soft_reset=soft, v_threshold=vth)
+        ref = spk.view(T, R, N // 4, 4).amax(-1)
+        assert s.shape == (T, R, N // 4) and torch.equal(s, ref)
+
+
+@pytest.mark.parametrize("pool", [False, True])
+@pytest.mark.parametrize("B,Cin,Cout", [(32, 512, 512), (8, 64, 96)])
+def test_dense_small_map_conv_matches_conv_kernel(pool, B, Cin, Cout):
+    """On a 2x2 map FusedConvBNLIFPool runs the conv as one dense Linear over
+    (pixel, channel) (no padding taps; the 2x2 max-pool as an OR of column
+    groups).  Its pre-activations equal a float64 conv of the same bf16
+    operands within fp32 accumulation error, and its spikes agree with the
+    direct conv kernel's (tile_hint forces that path) at >= 99.9%, every flip
+    next to the threshold."""
+    import torch.nn as nn
+    from snnk.kernels.conv import conv3x3_dense_weight
+    T, H, W = 4, 2, 2
+    g = torch.Generator().manual_seed(B + Cin + Cout + pool)
+    conv = nn.Conv2d(Cin, Cout, 3, padding=1)
+    with torch.no_grad():
+        conv.weight.copy_(torch.randn(Cout, Cin, 3, 3, generator=g) * (2.0 / (9 * Cin)) ** 0.5 * 3)
+        conv.bias.copy_(torch.randn(Cout, generator=g) * 0.1)
+    mod = snn.FusedConvBNLIFPool(conv, None, pool="max" if pool else None, neuron="lif",
+                                 tau=2.0, v_threshold=1.0).to(DEV)
+    x = (torch.rand(T, B, H, W, Cin, generator=g) < 0.3).to(torch.bfloat16)
+    xd = x.to(DEV)
+    dense = mod.forward_nhwc(xd).cpu().float()
+    direct = mod.forward_nhwc(xd, tile_hint=3).cpu().float()
+    assert dense.shape == direct.shape
+    assert (dense == direct).float().mean().item() >= 0.999
+    # pre-activations of the dense form against float64
+    w_d, b_d = conv3x3_dense_weight(mod.weight, mod.bias, H, W, pool)
+    pre = linear_preact(xd.reshape(T, B, -1), w_d, b_d).cpu().double()
+    wb = mod.weight.cpu().to(torch.bfloat16).double()
+    ref = F.conv2d(x.double().reshape(T * B, H, W, Cin).permute(0, 3, 1, 2), wb,
+                   mod.bias.cpu().double(), padding=1)  # [TB, Cout, H, W]
+    bound = F.conv2d(x.double().reshape(T * B, H, W, Cin).permute(0, 3, 1, 2), wb.abs(),
+                     padding=1)
+    if pool:
+        ref = ref.reshape(T, B, Cout, H * W).reshape(T, B, -1)
+        bound = bound.reshape(T, B, Cout, H * W).reshape(T, B, -1)
+    else:
+        ref = ref.permute(0, 2, 3, 1).reshape(T, B, -1)
+        bound = bound.permute(0, 2, 3, 1).reshape(T, B, -1)
+    assert torch.all((pre - ref).abs() <= 3e-5 * bound + 1e-6)
+    # the dense path's spikes are exactly the LIF (+ column OR) of those sums
+    spk, _, _ = on.lif_multistep(pre.float(), neuron="lif", v_threshold=1.0)
+    if pool:
+        spk = spk.view(T, B, Cout, 4).amax(-1).view(T, B, 1, 1, Cout)
+    else:
+        spk = spk.view(T, B, H, W, Cout)
+    assert torch.equal(dense, spk)

@@ -223,7 +223,7 @@ void conv3x3_kernel(ConvArgs a) {
       const bool row_ok = quad < a.n_quads;
       uint32_t ok = 0;
       if (row_ok) {
-        if constexpr (POOL) {
+        if constexpr (POOL && TAPS == 9) {
           b = static_cast<int>(fdiv(static_cast<uint32_t>(quad), a.div_howo));
           const int r2 = quad - b * a.Ho * a.Wo;
           const int py = static_cast<int>(fdiv(static_cast<uint32_t>(r2), a.div_wo));
@@ -293,8 +293,14 @@ void conv3x3_kernel(ConvArgs a) {
       for (int j = 0; j < TN; ++j) {
         if (!col_ok[j]) continue;
         const int n = n0 + (wn * TN + j) * 32 + r_lane;
+        // TAPS = 1 with POOL: the output keeps one column of every group of
+        // four adjacent columns (their OR), Cout / 4 columns per row
+        constexpr bool kColPool = POOL && TAPS == 1;
+        const int o_cols = kColPool ? a.Cout / 4 : a.Cout;
         uint16_t* o = a.out + static_cast<int64_t>(tc) * 4 * a.o_tstride +
-                      static_cast<int64_t>(POOL ? quad : quad * 4) * a.Cout + n;
+                      (POOL && !kColPool ? static_cast<int64_t>(quad) * a.Cout + n
+                                         : static_cast<int64_t>(quad) * 4 * o_cols +
+                                               (kColPool ? n / 4 : n));
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           if (tc * 4 + t >= a.T) break;
@@ -310,7 +316,16 @@ void conv3x3_kernel(ConvArgs a) {
             sp[q] = s;
             any = any || s;
           }
-          if constexpr (POOL) {
+          if constexpr (kColPool) {
+            // lanes 4k..4k+3 hold adjacent columns of the same rows
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              int sq = sp[q] ? 1 : 0;
+              sq |= __shfl_xor(sq, 1, 64);
+              sq |= __shfl_xor(sq, 2, 64);
+              if ((r_lane & 3) == 0) o[q * o_cols] = spike_bf16(sq != 0);
+            }
+          } else if constexpr (POOL) {
             o[0] = spike_bf16(any);
           } else {
 #pragma unroll
@@ -670,7 +685,8 @@ void auto_cfg_split(const ConvArgs& a, int* cfg, int* splits) {
     if (K >= 4096) { *cfg = 3; *splits = 4; }                         // 64 x 128, 4 splits
   } else if (rows <= 128) {
     if (a.Cout <= 64) { *cfg = 4; *splits = 4; }                      // 32 x 32
-    else if (K > 1024) { *cfg = 13; *splits = 2; }                    // 32 x 64
+    else if (K > 2048 || (K > 1024 && a.Cout > 2048)) { *cfg = 13; *splits = 2; }  // 32 x 64
+    else if (K > 1024) { *cfg = 4; *splits = 1; }  // 32 x 32, 4 K groups: 2x2 maps as Linear
   }
 }
 
@@ -820,7 +836,7 @@ int conv_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_t*
 int linear_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_t* spikes_out,
                 float* preact_out, int64_t T, int64_t R, int64_t K, int64_t N, float decay,
                 float in_scale, float v_threshold, float v_reset, int32_t soft_reset,
-                bool check_ptrs, ConvArgs* out) {
+                bool check_ptrs, ConvArgs* out, bool col_pool = false) {
   if (T < 0 || R < 0 || K <= 0 || N <= 0) return SNNK_EINVAL;
   if (check_ptrs) {
     if (x == nullptr || w == nullptr) return SNNK_EINVAL;
@@ -842,7 +858,7 @@ int linear_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_
   a.x_tstride_b = static_cast<uint32_t>(R * K * 2);
   a.x_bytes = static_cast<uint32_t>(T * R * K * 2);
   a.w_bytes = static_cast<uint32_t>(N * K * 2);
-  a.o_tstride = R * N;
+  a.o_tstride = col_pool ? R * (N / 4) : R * N;
   a.decay = decay; a.in_scale = in_scale; a.vth = v_threshold; a.v_reset = v_reset;
   a.soft_reset = soft_reset ? 1 : 0;
   *out = a;
@@ -860,6 +876,7 @@ int run(const ConvArgs& a, bool pool, int tile_hint, int splits, bool allow_spli
   if (p.ws_bytes > 0 && !aligned(ws, 256)) return SNNK_EALIGN;
   if constexpr (TAPS == 1) {
     if (mean) return dispatch<false, MODE_MEAN, 1>(a, p, ws, s);
+    if (pool) return dispatch<true, MODE_LIF, 1>(a, p, ws, s);  // OR of column groups of 4
   }
   if (a.pre != nullptr) return dispatch<false, MODE_PREACT, TAPS>(a, p, ws, s);
   if (pool) return dispatch<true, MODE_LIF, TAPS>(a, p, ws, s);
@@ -943,6 +960,23 @@ extern "C" int snnk_linear_bias_lif_ws(const uint16_t* x, const uint16_t* w, con
                        v_threshold, v_reset, soft_reset, true, &a);
   if (st != SNNK_OK) return st;
   return run<1>(a, false, tile_hint, splits, true, workspace, workspace_bytes,
+                static_cast<hipStream_t>(stream));
+}
+
+extern "C" int snnk_linear_bias_lif_pool4_ws(const uint16_t* x, const uint16_t* w,
+                                             const float* bias, uint16_t* spikes_out, int64_t T,
+                                             int64_t R, int64_t K, int64_t N, float decay,
+                                             float in_scale, float v_threshold, float v_reset,
+                                             int32_t soft_reset, int32_t tile_hint,
+                                             int32_t splits, void* workspace,
+                                             int64_t workspace_bytes, void* stream) {
+  if (T == 0 || R == 0) return (T < 0 || R < 0) ? SNNK_EINVAL : SNNK_OK;
+  if (spikes_out == nullptr) return SNNK_EINVAL;
+  ConvArgs a;
+  int st = linear_args(x, w, bias, spikes_out, nullptr, T, R, K, N, decay, in_scale,
+                       v_threshold, v_reset, soft_reset, true, &a, true);
+  if (st != SNNK_OK) return st;
+  return run<1>(a, true, tile_hint, splits, true, workspace, workspace_bytes,
                 static_cast<hipStream_t>(stream));
 }
 

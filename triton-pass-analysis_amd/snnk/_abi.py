@@ -94,6 +94,14 @@ PROTOTYPES: dict[str, list] = {
         _i32, _p, _i64,        # splits, workspace, workspace_bytes
         _p,                    # stream
     ],
+    "snnk_linear_bias_lif_pool4_ws": [
+        _p, _p, _p, _p,        # x, w, bias, spikes_out
+        _i64, _i64, _i64, _i64,  # T, R, K, N
+        _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
+        _i32, _i32,            # soft_reset, tile_hint
+        _i32, _p, _i64,        # splits, workspace, workspace_bytes
+        _p,                    # stream
+    ],
     "snnk_linear_mean_t": [
         _p, _p, _p, _p,        # x, w, bias, out
         _i64, _i64, _i64, _i64,  # T, R, K, N

@@ -25,6 +25,37 @@ def prepare_conv3x3_weight(weight: torch.Tensor) -> torch.Tensor:
     return weight.permute(0, 2, 3, 1).reshape(Cout, 9 * Cin).to(torch.bfloat16).contiguous()
 
 
+def conv3x3_dense_weight(weight: torch.Tensor, bias: torch.Tensor | None, H: int, W: int,
+                         pool: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """A 3x3 / pad 1 conv on an H x W map (H, W <= 2) as one dense matrix.
+
+    On such a map every output pixel sees every input pixel through one tap,
+    so conv(x)[po, co] = sum_{pi, ci} x[pi, ci] * w[co, ci, yi - yo + 1,
+    xi - xo + 1]: a Linear over the flattened NHWC map with K = H*W*Cin
+    (the padding taps, zero by definition, drop out).  Returns bf16
+    ``[N, H*W*Cin]`` and fp32 bias ``[N]`` with the output columns in
+    (pixel, cout) order -- NHWC -- or, with ``pool`` (a 2x2 map), in (cout,
+    pixel) order so that the 2x2 max-pool is the OR of four adjacent columns.
+    """
+    assert weight.ndim == 4 and weight.shape[2:] == (3, 3) and H <= 2 and W <= 2
+    assert not pool or (H == 2 and W == 2)
+    Cout, Cin = weight.shape[:2]
+    P = H * W
+    w = weight.float()
+    dense = torch.empty(P, Cout, P, Cin, device=w.device, dtype=torch.float32)  # [po, co, pi, ci]
+    for po in range(P):
+        yo, xo = divmod(po, W)
+        for pi in range(P):
+            yi, xi = divmod(pi, W)
+            dense[po, :, pi, :] = w[:, :, yi - yo + 1, xi - xo + 1]
+    if pool:
+        dense = dense.permute(1, 0, 2, 3)  # [co, po, pi, ci]
+    b = bias.float() if bias is not None else torch.zeros(Cout, device=w.device)
+    b_dense = b.repeat_interleave(P) if pool else b.repeat(P)
+    return (dense.reshape(P * Cout, P * Cin).to(torch.bfloat16).contiguous(),
+            b_dense.contiguous())
+
+
 def to_nhwc_bf16(x_seq: torch.Tensor) -> torch.Tensor:
     """[T, B, C, H, W] (any memory format, fp32/bf16/fp16/uint8) -> contiguous NHWC bf16
     ``[T, B, H, W, C]``.  A bf16 channels-last input is returned as a view, any

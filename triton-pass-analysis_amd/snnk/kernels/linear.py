@@ -66,6 +66,33 @@ def _linear_call(x, w, bias, out, pre, decay, in_scale, v_threshold, v_reset, so
                   sp, _abi.ptr(ws), 0 if ws is None else ws.numel(), _abi.stream(x.device))
 
 
+def linear_bias_lif_pool4(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
+                          decay: float, in_scale: float, v_threshold: float,
+                          v_reset: float = 0.0, soft_reset: bool = False,
+                          out: torch.Tensor | None = None, tile_hint: int = -1,
+                          splits: int | None = None) -> torch.Tensor:
+    """x [T, R, K] bf16, w [N, K] bf16 -> spikes [T, R, N // 4] bf16: Linear +
+    bias + LIF per column, then the OR (max) of each group of four adjacent
+    columns, in one kernel."""
+    _check(x, w, bias)
+    T, R, K = x.shape
+    N = w.shape[0]
+    assert N % 4 == 0
+    if out is None:
+        out = torch.empty(T, R, N // 4, device=x.device, dtype=torch.bfloat16)
+    else:
+        assert out.shape == (T, R, N // 4) and out.dtype == torch.bfloat16 and out.is_contiguous()
+    sp = 0 if splits is None else int(splits)
+    with torch.cuda.device(x.device):
+        nbytes = _abi.size_call("snnk_linear_bias_lif_ws_size", T, R, K, N, 0, int(tile_hint), sp)
+        ws = _workspace.get(x.device, nbytes)
+        _abi.call("snnk_linear_bias_lif_pool4_ws", x.data_ptr(), w.data_ptr(), _abi.ptr(bias),
+                  out.data_ptr(), T, R, K, N, float(decay), float(in_scale), float(v_threshold),
+                  float(v_reset), 1 if soft_reset else 0, int(tile_hint), sp, _abi.ptr(ws),
+                  0 if ws is None else ws.numel(), _abi.stream(x.device))
+    return out
+
+
 def linear_preact(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
                   out: torch.Tensor | None = None, tile_hint: int = -1,
                   splits: int | None = None) -> torch.Tensor:

@@ -16,9 +16,9 @@ from ..kernels.fused import (
     fused_bias_if_lif, fused_bias_if_lif_rate, fused_bias_if_lif_stateful, fold_conv_bn,
 )
 from ..kernels.conv import (
-    prepare_conv3x3_weight, to_nhwc_bf16, conv3x3_bn_lif_nhwc,
+    prepare_conv3x3_weight, to_nhwc_bf16, conv3x3_bn_lif_nhwc, conv3x3_dense_weight,
 )
-from ..kernels.linear import linear_bias_lif, linear_fusable
+from ..kernels.linear import linear_bias_lif, linear_bias_lif_pool4, linear_fusable
 
 
 def _thr(module, v_threshold):
@@ -324,11 +324,36 @@ class FusedConvBNLIFPool(nn.Module):
         self.decay_factor, self.input_scale = neuron_params(neuron, tau, decay, decay_input)
         self.soft_reset, self.v_threshold, self.v_reset = soft_reset, float(v_threshold), v_reset
 
+    def _dense(self, H, W):
+        """Dense-matrix form of the conv for a map of at most 2x2 (built once
+        per map size, on the weights' device)."""
+        key = (H, W)
+        cache = self.__dict__.setdefault("_dense_cache", {})
+        if key not in cache:
+            cache[key] = conv3x3_dense_weight(self.weight, self.bias, H, W, self.pool == "max")
+        return cache[key]
+
     def forward_nhwc(self, x_nhwc, out=None, tile_hint=-1):
+        T, B, H, W, C = x_nhwc.shape
+        lif = dict(decay=self.decay_factor, in_scale=self.input_scale,
+                   v_threshold=self.v_threshold, v_reset=self.v_reset,
+                   soft_reset=self.soft_reset)
+        if H <= 2 and W <= 2 and B % 4 == 0 and tile_hint < 0 and \
+                (self.pool != "max" or (H == 2 and W == 2)):
+            # every output pixel sees the whole map: one dense Linear + LIF
+            # (+ the pool as an OR of column groups), no padding taps
+            w_d, b_d = self._dense(H, W)
+            x2 = x_nhwc.reshape(T, B, H * W * C)
+            Cout = self.weight.shape[0]
+            if self.pool == "max":
+                o2 = None if out is None else out.view(T, B, Cout)
+                y = linear_bias_lif_pool4(x2, w_d, b_d, out=o2, **lif)
+                return y.view(T, B, 1, 1, Cout)
+            o2 = None if out is None else out.view(T, B, H * W * Cout)
+            y = linear_bias_lif(x2, w_d, b_d, out=o2, **lif)
+            return y.view(T, B, H, W, Cout)
         return conv3x3_bn_lif_nhwc(x_nhwc, self.w_prep, self.bias, pool=self.pool == "max",
-                                   decay=self.decay_factor, in_scale=self.input_scale,
-                                   v_threshold=self.v_threshold, v_reset=self.v_reset,
-                                   soft_reset=self.soft_reset, out=out, tile_hint=tile_hint)
+                                   out=out, tile_hint=tile_hint, **lif)
 
     def forward(self, x_seq):
         s = self.forward_nhwc(to_nhwc_bf16(x_seq)).permute(0, 1, 4, 2, 3)
