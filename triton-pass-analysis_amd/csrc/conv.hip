@@ -664,6 +664,7 @@ int auto_cfg(const ConvArgs& a) {
   const int64_t K = static_cast<int64_t>(a.n_stages) * kKS;
   if (rows >= 65536) return 1;                                        // 256 x 64
   if (rows >= 32768) return a.Cout >= 256 ? 14 : (K <= 576 ? 3 : 9);
+  if (rows >= 8192 && K <= 512) return a.Cout <= 512 ? 9 : 2;        // short K (SSA projections)
   if (rows >= 8192) return 3;                                         // 64 x 128
   if (rows >= 2048) return 8;                                         // 32 x 128 split-K 4
   if (rows >= 512) return 4;                                          // 32 x 32 split-K 4
@@ -683,6 +684,8 @@ void auto_cfg_split(const ConvArgs& a, int* cfg, int* splits) {
   if (rows > 2048 || rows < 16) return;
   if (rows > 512) {
     if (K >= 4096) { *cfg = 3; *splits = 4; }                         // 64 x 128, 4 splits
+  } else if (rows > 128 && rows <= 256) {
+    if (K > 1024 && K <= 2048 && a.Cout <= 2048) { *cfg = 5; *splits = 2; }  // 32 x 128
   } else if (rows <= 128) {
     if (a.Cout <= 64) { *cfg = 4; *splits = 4; }                      // 32 x 32
     else if (K > 2048 || (K > 1024 && a.Cout > 2048)) { *cfg = 13; *splits = 2; }  // 32 x 64
