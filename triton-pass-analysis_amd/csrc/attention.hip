@@ -9,7 +9,7 @@
 // (Q K^T) V order and can return both count tensors for bit-exact checks.
 //
 // One block per (batch, head).  Per step t the block stages Q_t,
-// K_t and V_t^T of its head in LDS as int8 (zero padded to 64 tokens x 64
+// K_t and V_t^T of its head in LDS as int8 (read from memory one step ahead) (zero padded to 64 tokens x 64
 // dims; d % 8 == 0, rows 16-byte aligned), computes S = Q K^T into accumulators, writes S to LDS as int8
 // (0 <= S <= d <= 64), computes O = S V, and runs the LIF
 // v = decay*v + in_scale*O on O in registers; the membrane of every
@@ -79,10 +79,13 @@ __global__ __launch_bounds__(256) void ssa_attention_kernel(AttnArgs a) {
 #pragma unroll
   for (int e = 0; e < 16; ++e) vm[e] = 0.0f;
 
-  for (int t = 0; t < a.T; ++t) {
-    // ---- stage Q_t, K_t (row = token) and V_t^T (row = dim) as int8 -------
-    // 64 tokens x 8 chunks of 8 dims per tensor; consecutive threads walk
-    // along a token row with 16-byte loads; padding rows / dims are zeros.
+  // ---- staging of Q_t, K_t (row = token) and V_t^T (row = dim) as int8 ----
+  // 64 tokens x 8 chunks of 8 dims per tensor; consecutive threads walk along
+  // a token row with 16-byte loads; padding rows / dims are zeros.  The loads
+  // of step t+1 are issued into registers before step t's MFMAs, so only the
+  // first step waits for memory.
+  u32x4 rq[2], rk[2], rv[2];
+  auto load_step = [&](int t) {
     const uint16_t* qt = qb + t * a.q_t;
     const uint16_t* kt = kb + t * a.k_t;
     const uint16_t* vtp = vb + t * a.v_t;
@@ -90,25 +93,37 @@ __global__ __launch_bounds__(256) void ssa_attention_kernel(AttnArgs a) {
     for (int m = 0; m < 2; ++m) {
       const int ci = tid + 256 * m;
       const int n = ci >> 3, c = ci & 7;
-      const bool in = n < a.N && c * 8 < a.d;
-      u32x4 wq = {0u, 0u, 0u, 0u}, wk = wq, wv = wq;
-      if (in) {
-        wq = *reinterpret_cast<const u32x4*>(qt + n * a.q_row + c * 8);
-        wk = *reinterpret_cast<const u32x4*>(kt + n * a.k_row + c * 8);
-        wv = *reinterpret_cast<const u32x4*>(vtp + n * a.v_row + c * 8);
+      rq[m] = rk[m] = rv[m] = u32x4{0u, 0u, 0u, 0u};
+      if (n < a.N && c * 8 < a.d) {
+        rq[m] = *reinterpret_cast<const u32x4*>(qt + n * a.q_row + c * 8);
+        rk[m] = *reinterpret_cast<const u32x4*>(kt + n * a.k_row + c * 8);
+        rv[m] = *reinterpret_cast<const u32x4*>(vtp + n * a.v_row + c * 8);
       }
+    }
+  };
+  auto store_step = [&]() {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int ci = tid + 256 * m;
+      const int n = ci >> 3, c = ci & 7;
       u32x2 bq, bk;
-      bq[0] = bytes4(wq[0], wq[1]); bq[1] = bytes4(wq[2], wq[3]);
-      bk[0] = bytes4(wk[0], wk[1]); bk[1] = bytes4(wk[2], wk[3]);
+      bq[0] = bytes4(rq[m][0], rq[m][1]); bq[1] = bytes4(rq[m][2], rq[m][3]);
+      bk[0] = bytes4(rk[m][0], rk[m][1]); bk[1] = bytes4(rk[m][2], rk[m][3]);
       *reinterpret_cast<u32x2*>(qs + n * kPitch + c * 8) = bq;
       *reinterpret_cast<u32x2*>(ks + n * kPitch + c * 8) = bk;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const uint32_t w = wv[e >> 1] >> (16 * (e & 1));
+        const uint32_t w = rv[m][e >> 1] >> (16 * (e & 1));
         vt[(c * 8 + e) * kPitch + n] = (w & 0x7FFFu) ? 1 : 0;
       }
     }
+  };
+
+  load_step(0);
+  for (int t = 0; t < a.T; ++t) {
+    store_step();
     __syncthreads();
+    if (t + 1 < a.T) load_step(t + 1);
 
     // ---- S = Q K^T (one 32x32 tile per wave) --------------------------------
     if (has_s) {
