@@ -474,8 +474,14 @@ extern "C" int snnk_binary_gemm(const uint32_t* A, const uint32_t* B, void* C, i
   }
   if (algo == SNNK_BGEMM_MFMA_F4 && K >= (1ll << 24)) return SNNK_EUNSUPPORTED;  // fp32 counts
   const int sel = (signed_w ? 4 : 0) | (c_dtype == SNNK_F32 ? 2 : 0) | (algo == SNNK_BGEMM_MFMA_F4 ? 1 : 0);
-#define SNNK_BGEMM_LAUNCH(S, F, X) \
-  launch_mfma<S, F, X>(A, B, C, batch, M, N, K, lda, ldb, ldc, stride_a, stride_b, stride_c, s)
+  // fp4: 128x128 wave tiles (one wave per SIMD, 256 accumulator registers,
+  // fewer unpacking ops per MFMA) once they still give every SIMD a wave
+  const bool big = batch * ((M + 127) / 128) * ((N + 127) / 128) >= 1024;
+#define SNNK_BGEMM_LAUNCH(S, F, X)                                                               \
+  ((X && big) ? launch_mfma<S, F, X, 4, 4>(A, B, C, batch, M, N, K, lda, ldb, ldc, stride_a,     \
+                                           stride_b, stride_c, s)                                \
+              : launch_mfma<S, F, X>(A, B, C, batch, M, N, K, lda, ldb, ldc, stride_a, stride_b, \
+                                     stride_c, s))
   switch (sel) {
     case 0: return SNNK_BGEMM_LAUNCH(false, false, false);
     case 1: return SNNK_BGEMM_LAUNCH(false, false, true);
