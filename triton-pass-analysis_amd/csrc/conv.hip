@@ -469,7 +469,9 @@ void conv3x3_kernel(ConvArgs a) {
       }
     };
 
-#pragma unroll
+    // a loop, not unrolled: this code runs once per launch from a cold
+    // instruction cache, so one copy of it is fetched instead of NBUF-1
+#pragma nounroll
     for (int p = 0; p < C::kBuf - 1; ++p) {
       const StageAddr sp = prepare(p);
 #pragma unroll

@@ -6,6 +6,8 @@ and adds it to every step, as the reference does.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 import torch.nn.functional as F
 
@@ -25,7 +27,7 @@ def _fused_C_HW(y_seq: torch.Tensor):
         return y_seq.shape[2], y_seq.shape[3]
     if y_seq.ndim == 3:
         return y_seq.shape[-1], 1
-    return y_seq[0].numel(), 1
+    return math.prod(y_seq.shape[1:]), 1
 
 
 def _fused_threshold(v_threshold, C: int, NCL: int, like: torch.Tensor):
@@ -67,7 +69,7 @@ def fused_bias_if_lif(
     """
     check_flat(y_seq, layout, "y_seq")
     assert y_seq.dtype in (torch.float32, torch.float16, torch.bfloat16)
-    NCL = y_seq[0].numel()
+    NCL = math.prod(y_seq.shape[1:])
     C, HW = _fused_C_HW(y_seq)
     df, sc = neuron_params(neuron, tau, decay, decay_input)
     thr = _fused_threshold(v_threshold, C, NCL, y_seq)
@@ -104,11 +106,13 @@ def fused_bias_if_lif_rate(
     """
     check_flat(y_seq, layout, "y_seq")
     assert y_seq.dtype in (torch.float32, torch.float16, torch.bfloat16)
-    NCL = y_seq[0].numel()
+    NCL = math.prod(y_seq.shape[1:])
     C, HW = _fused_C_HW(y_seq)
     df, sc = neuron_params(neuron, tau, decay, decay_input)
     thr = _fused_threshold(v_threshold, C, NCL, y_seq)
     _check_bias(bias, C)
+    if y_seq.shape[0] == 0:  # no steps: no spikes
+        return torch.zeros(y_seq.shape[1:], device=y_seq.device, dtype=torch.float32)
     count = torch.empty_like(y_seq[0], dtype=torch.float32)
     launch_lif(y_seq, bias=bias, thr=thr, count=count, C=C, HW=HW,
                channel_last=(layout == "NHWC"), decay=df, in_scale=sc,
@@ -139,7 +143,7 @@ def fused_bias_if_lif_stateful(
     """
     check_flat(y_seq, layout, "y_seq")
     assert y_seq.dtype in (torch.float32, torch.float16, torch.bfloat16)
-    NCL = y_seq[0].numel()
+    NCL = math.prod(y_seq.shape[1:])
     C, HW = _fused_C_HW(y_seq)
     df, sc = neuron_params(neuron, tau, decay, decay_input)
     _check_bias(bias, C)
@@ -151,6 +155,11 @@ def fused_bias_if_lif_stateful(
     v_out = torch.empty(y_seq.shape[1:], device=y_seq.device, dtype=torch.float32) \
         if return_v else None
     spike = torch.empty_like(y_seq)
+    if y_seq.shape[0] == 0:  # no steps: the membrane stays where it was
+        if return_v:
+            v_out.copy_(v_init.view(v_out.shape) if v_init is not None else torch.zeros_like(v_out))
+            return spike, v_out
+        return spike
     launch_lif(y_seq, bias=bias, thr=(THR_SCALAR, None, float(v_threshold)),
                v_init=v_in, v_out=v_out, spikes=spike, C=C, HW=HW,
                channel_last=(layout == "NHWC"), decay=df, in_scale=sc,

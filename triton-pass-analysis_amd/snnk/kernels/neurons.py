@@ -9,6 +9,8 @@ The membrane recurrence itself runs in ``snnk_lif_forward`` (csrc/lif.hip).
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from .. import _abi
@@ -84,9 +86,9 @@ def check_flat(x: torch.Tensor, layout: str, what: str = "x_seq") -> None:
         return
     assert layout == "NHWC", \
         f"non-contiguous {what} requires layout='NHWC', got {layout}"
-    ok = x.ndim == 5 and x.stride(0) == x[0].numel() and \
+    ok = x.ndim == 5 and x.stride(0) == math.prod(x.shape[1:]) and \
         x[0].is_contiguous(memory_format=torch.channels_last)
-    ok = ok or (x.ndim == 4 and x.stride(0) == x[0].numel()
+    ok = ok or (x.ndim == 4 and x.stride(0) == math.prod(x.shape[1:])
                 and x.permute(0, 1, 3, 2).is_contiguous())
     assert ok, f"{what} with layout='NHWC' must be dense channels-last per step"
 
@@ -98,7 +100,7 @@ def launch_lif(x, *, bias=None, residual=None, thr=(THR_SCALAR, None, 1.0),
     """Enqueue snnk_lif_forward on the current stream of ``x``'s device.
     An int32 ``spikes`` tensor receives packed bits ([T, NCL/32] words)."""
     T = x.shape[0]
-    NCL = x[0].numel() if T > 0 else 0
+    NCL = math.prod(x.shape[1:])
     thr_mode, thr_t, thr_s = thr
     sfmt = _abi.SPIKE_SAME
     if spikes is not None and spikes.dtype != x.dtype:
@@ -141,7 +143,7 @@ def if_lif(
     """
     check_flat(x_seq, layout)
     assert x_seq.dtype in (torch.float32, torch.float16, torch.bfloat16)
-    NCL = x_seq[0].numel()
+    NCL = math.prod(x_seq.shape[1:])
     C, HW = infer_C_HW(x_seq)
     df, sc = neuron_params(neuron, tau, decay, decay_input)
     Cthr = x_seq.shape[2] if x_seq.ndim >= 4 else (x_seq.shape[-1] if x_seq.ndim == 3 else 1)
@@ -179,7 +181,7 @@ def if_lif_packed(
     check_flat(x_seq, layout)
     assert x_seq.dtype in (torch.float32, torch.float16, torch.bfloat16)
     T = x_seq.shape[0]
-    NCL = x_seq[0].numel()
+    NCL = math.prod(x_seq.shape[1:])
     if NCL % 32 != 0:
         raise ValueError(f"packed spikes need NCL % 32 == 0, got NCL={NCL}")
     C, HW = infer_C_HW(x_seq)
