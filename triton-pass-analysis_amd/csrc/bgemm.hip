@@ -81,6 +81,66 @@ __device__ __forceinline__ void mfma_stage(i32x16 (&acc)[TM][TN], const u32x4 (&
   }
 }
 
+// Largest row pitch (elements) of C for which every offset inside a
+// 128-row tile fits the 32-bit buffer offsets of store_tile's fast path.
+constexpr int64_t kMaxFastLdc = int64_t{1} << 22;
+
+// Writes a wave's TM x TN tiles of 32x32 counts (SIGNED: 2*count - rowpop).
+// Accumulator register e of lane l holds row 8*(e/4) + 4*(l/32) + e%4,
+// column l%32 of its tile.  A wave tile wholly inside C (every tile of a
+// shape that the tiles divide) is written by buffer stores whose row offset
+// is wave-uniform (an SGPR) and whose column offset is an immediate: no
+// per-element bounds branch and no 64-bit address arithmetic (3.5 KB of code
+// for a 128x128 fp4 tile against 17 KB for the checked path, which every
+// launch would fetch from a cold instruction cache).
+template <bool SIGNED, bool OUT_F32, int TM, int TN, typename Acc>
+__device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], const int (&rowpop)[TM],
+                                           void* Cb, int64_t M, int64_t N, int64_t ldc,
+                                           int64_t m_base, int64_t n_base, int lane) {
+  const int r32 = lane & 31, g = lane >> 5;
+  auto value = [&](int i, int j, int e, int rp) __attribute__((always_inline)) {
+    int32_t c = static_cast<int32_t>(acc[i][j][e]);  // exact integer count
+    if constexpr (SIGNED) c = 2 * c - rp;
+    if constexpr (OUT_F32) return __float_as_uint(static_cast<float>(c));
+    else return static_cast<uint32_t>(c);
+  };
+  if (m_base + 32 * TM <= M && n_base + 32 * TN <= N && ldc <= kMaxFastLdc) {
+    uint32_t* base = static_cast<uint32_t*>(Cb) + m_base * ldc + n_base;
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(base, 0, -1, kRsrcWord3);
+    const uint32_t ldc4 = static_cast<uint32_t>(ldc) * 4u;
+    const uint32_t voff = static_cast<uint32_t>(4 * g) * ldc4 + static_cast<uint32_t>(r32) * 4u;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        int rp = 0;
+        if constexpr (SIGNED) rp = __shfl(rowpop[i], 8 * (e >> 2) + 4 * g + (e & 3), 64);
+        const uint32_t soff = static_cast<uint32_t>(i * 32 + 8 * (e >> 2) + (e & 3)) * ldc4;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)  // non-temporal (aux bit 1): the counts are not re-read here
+          __builtin_amdgcn_raw_buffer_store_b32(value(i, j, e, rp), rc, voff + j * 128, soff, 2);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int rr = 8 * (e >> 2) + 4 * g + (e & 3);
+      int rp = 0;
+      if constexpr (SIGNED) rp = __shfl(rowpop[i], rr, 64);
+      const int64_t m = m_base + i * 32 + rr;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t n = n_base + j * 32 + r32;
+        if (m < M && n < N)
+          __builtin_nontemporal_store(value(i, j, e, rp), static_cast<uint32_t*>(Cb) + m * ldc + n);
+      }
+    }
+  }
+}
+
 // One wave per workgroup.  The packed words of each stage (4 per row: 16
 // bytes for each of the 32*TM A rows and 32*TN B rows) arrive by direct
 // global->LDS buffer loads into a kRing-deep ring, kRing-1 stages ahead, so
@@ -180,32 +240,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<TM, TN>()))) void bgemm_mfma_k
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // trailing zero-fill loads
 
-  // Epilogue.  Accumulator register e of lane l holds row 8*(e/4) + 4*g + e%4,
-  // column l%32 of its 32x32 tile.
-  void* Cb = OUT_F32 ? static_cast<void*>(static_cast<float*>(Cv) + bz * sC)
-                     : static_cast<void*>(static_cast<int32_t*>(Cv) + bz * sC);
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int rr = 8 * (e >> 2) + 4 * g + (e & 3);
-      int rp = 0;
-      if constexpr (SIGNED) rp = __shfl(rowpop[i], rr, 64);
-      const int64_t m = m_base + i * 32 + rr;
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int64_t n = n_base + j * 32 + r32;
-        if (m < M && n < N) {
-          int32_t c = acc[i][j][e];
-          if constexpr (SIGNED) c = 2 * c - rp;
-          if constexpr (OUT_F32)
-            __builtin_nontemporal_store(static_cast<float>(c), static_cast<float*>(Cb) + m * ldc + n);
-          else
-            __builtin_nontemporal_store(c, static_cast<int32_t*>(Cb) + m * ldc + n);
-        }
-      }
-    }
-  }
+  // C elements are 4 bytes (int32 or fp32) either way
+  store_tile<SIGNED, OUT_F32, TM, TN>(acc, rowpop, static_cast<uint32_t*>(Cv) + bz * sC, M, N, ldc,
+                                      m_base, n_base, lane);
 }
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
@@ -388,30 +425,8 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<TM, TN>()))) void bgemm_f4_ker
 #pragma unroll
     for (int t = 0; t < TM; ++t) rowpop[t] += __shfl_xor(rowpop[t], 32, 64);
   }
-  void* Cb = OUT_F32 ? static_cast<void*>(static_cast<float*>(Cv) + bz * sC)
-                     : static_cast<void*>(static_cast<int32_t*>(Cv) + bz * sC);
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int rr = 8 * (e >> 2) + 4 * g + (e & 3);
-      int rp = 0;
-      if constexpr (SIGNED) rp = __shfl(rowpop[i], rr, 64);
-      const int64_t m = m_base + i * 32 + rr;
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int64_t n = n_base + j * 32 + r32;
-        if (m < M && n < N) {
-          int32_t c = static_cast<int32_t>(acc[i][j][e]);  // exact integer count
-          if constexpr (SIGNED) c = 2 * c - rp;
-          if constexpr (OUT_F32)
-            __builtin_nontemporal_store(static_cast<float>(c), static_cast<float*>(Cb) + m * ldc + n);
-          else
-            __builtin_nontemporal_store(c, static_cast<int32_t*>(Cb) + m * ldc + n);
-        }
-      }
-    }
-  }
+  store_tile<SIGNED, OUT_F32, TM, TN>(acc, rowpop, static_cast<uint32_t*>(Cv) + bz * sC, M, N, ldc,
+                                      m_base, n_base, lane);
 }
 
 // 64x128 wave tiles, two waves per SIMD: 8192x4096x4096 in 111 us against
