@@ -41,6 +41,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -49,6 +50,9 @@ constexpr int kRow = kKS;         // LDS row pitch in bf16 (128 B, eight 16-byte
 constexpr int kRowBytes = kRow * 2;
 constexpr int kDmaRows = 1024 / kRowBytes;  // rows filled by one wave-wide 16-byte load
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
+// buffer-access cache policy sc0 | sc1: system-coherent, through to memory
+// past the XCD's L2 (the split-K partial sums of blocks on other XCDs)
+constexpr int kSystemCoherent = 17;
 // Offset base past every operand: kFar plus any stage delta (< 2^31) stays
 // below 2^32 and at or past the end of an operand of at most kFar bytes, so
 // such a load reads zeros (padding taps, rows past the end, steps past T,
@@ -187,6 +191,7 @@ void conv3x3_kernel(ConvArgs a) {
   const int st_begin = split * a.stages_per_split;
   const int st_end = min(a.n_stages, st_begin + a.stages_per_split);
   const int HW = a.H * a.W;
+  constexpr int kPartFloats = TM * TN * 16 * 64;  // a wave's share of an output tile
   const int K = TAPS * a.Cin;
 
   // Operands are read through range-checked buffer descriptors: an offset
@@ -574,17 +579,24 @@ void conv3x3_kernel(ConvArgs a) {
       if (a.splits == 1) {
         epilogue(acc, tc);
       } else {
-        float* dst = a.partials + ((static_cast<int64_t>(mn) * a.splits + split) * n_chunks + tc) *
-                                      (C::BM * C::BN) + wmn * (TM * TN * 16 * 64) + lane;
+        // this block's partial sums: 16-byte pieces, system-coherent (written
+        // through to memory, past this XCD's L2)
+        const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+            a.partials + (static_cast<int64_t>(mn) * a.splits + split) * n_chunks * (C::BM * C::BN),
+            0, -1, kRsrcWord3);
+        const uint32_t voff = static_cast<uint32_t>(tc * (C::BM * C::BN) + wmn * kPartFloats) * 4u +
+                              static_cast<uint32_t>(lane) * 16u;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-              // system-coherent store: written through to memory, past this XCD's L2
-              __hip_atomic_store(dst + ((i * TN + j) * 16 + e) * 64, acc[i][j][e],
-                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            for (int q = 0; q < 4; ++q) {
+              const i32x4 v = {__float_as_int(acc[i][j][4 * q]), __float_as_int(acc[i][j][4 * q + 1]),
+                               __float_as_int(acc[i][j][4 * q + 2]), __float_as_int(acc[i][j][4 * q + 3])};
+              __builtin_amdgcn_raw_buffer_store_b128(v, pr, voff + ((i * TN + j) * 4 + q) * 1024, 0,
+                                                     kSystemCoherent);
+            }
       }
     }
   }
@@ -606,28 +618,36 @@ void conv3x3_kernel(ConvArgs a) {
     __syncthreads();
     if (!*s_last) return;
     if (kg == 0) {
-      for (int tc = 0; tc < n_chunks; ++tc) {
-        f32x16 acc[TM][TN];
-        const float* src = a.partials + static_cast<int64_t>(mn) * a.splits * n_chunks * (C::BM * C::BN) +
-                           static_cast<int64_t>(tc) * (C::BM * C::BN) + wmn * (TM * TN * 16 * 64) + lane;
+      // the tile's partial sums, read back with system-coherent 16-byte loads
+      const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+          a.partials + static_cast<int64_t>(mn) * a.splits * n_chunks * (C::BM * C::BN), 0, -1,
+          kRsrcWord3);
+      const uint32_t split_bytes = static_cast<uint32_t>(n_chunks * (C::BM * C::BN)) * 4u;
+      auto load_part = [&](f32x16 (&dst)[TM][TN], uint32_t voff) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-              acc[i][j][e] = __hip_atomic_load(src + ((i * TN + j) * 16 + e) * 64, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_SYSTEM);
+            for (int q = 0; q < 4; ++q) {
+              const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+                  pr, voff + ((i * TN + j) * 4 + q) * 1024, 0, kSystemCoherent);
+#pragma unroll
+              for (int c = 0; c < 4; ++c) dst[i][j][4 * q + c] = __int_as_float(v[c]);
+            }
+      };
+      for (int tc = 0; tc < n_chunks; ++tc) {
+        const uint32_t voff = static_cast<uint32_t>(tc * (C::BM * C::BN) + wmn * kPartFloats) * 4u +
+                              static_cast<uint32_t>(lane) * 16u;
+        f32x16 acc[TM][TN];
+        load_part(acc, voff);
         for (int sp = 1; sp < a.splits; ++sp) {  // fixed summation order
-          const float* p = src + static_cast<int64_t>(sp) * n_chunks * (C::BM * C::BN);
+          f32x16 part[TM][TN];
+          load_part(part, voff + sp * split_bytes);
 #pragma unroll
           for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-              for (int e = 0; e < 16; ++e)
-                acc[i][j][e] += __hip_atomic_load(p + ((i * TN + j) * 16 + e) * 64, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_SYSTEM);
+            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
         }
         epilogue(acc, tc);
       }
@@ -724,6 +744,9 @@ int make_plan(const ConvArgs& a, int tile_hint, int splits_hint, bool allow_spli
     // at least 4 K stages per split; tile ids must fit the ticket region
     splits = std::max(1, std::min(splits, a.n_stages / 4));
     if (mn > kMaxTickets) splits = 1;
+    // a tile's partial sums are addressed with 32-bit byte offsets
+    const int64_t tile_part_bytes = static_cast<int64_t>((a.T + 3) / 4) * ts.bm * ts.bn * 4;
+    if (splits * tile_part_bytes >= (int64_t{1} << 32)) splits = 1;
   }
   p->stages_per_split = (a.n_stages + splits - 1) / splits;
   p->splits = (a.n_stages + p->stages_per_split - 1) / p->stages_per_split;  // none empty
