@@ -114,6 +114,29 @@ def test_conv_block_baseline_config():
     assert not torch.any((got != ref) & ~near)
 
 
+@pytest.mark.parametrize("B", [1, 32, 56])
+def test_image_layer_run_lengths(B):
+    """32x32 images at the batch sizes that select runs of 1, 2 and 4 pixels
+    per thread: spikes match the fp64 conv + LIF except where the membrane
+    came within 1e-5 of the threshold at this step or an earlier one (a flip
+    there changes the neuron's later reset history)."""
+    g = torch.Generator().manual_seed(40 + B)
+    img = torch.randn(B, 3, 32, 32, generator=g)
+    w = torch.randn(64, 3, 3, 3, generator=g) * (2.0 / 27) ** 0.5
+    b = torch.randn(64, generator=g) * 0.1
+    T = 4
+    spk = kc.conv3x3_image_lif(img.to(DEV), w.to(DEV), b.to(DEV), T, decay=0.5,
+                               in_scale=0.5, v_threshold=1.0)
+    y = F.conv2d(img.double(), w.double(), b.double(), padding=1).float()
+    yt = y.unsqueeze(0).expand(T, *y.shape).contiguous()
+    ref, _, _ = on.lif_multistep(yt, neuron="lif")
+    hs = of.membrane_trace(yt)
+    got = spk.cpu().float().permute(0, 1, 4, 2, 3)
+    near = torch.cummax(((hs - 1.0).abs() < 1e-5).int(), dim=0).values.bool()
+    assert not torch.any((got != ref) & ~near)
+    assert 0.01 < got.mean().item() < 0.99
+
+
 def test_image_layer_and_layout():
     g = torch.Generator().manual_seed(4)
     img = torch.randn(3, 3, 12, 10, generator=g)

@@ -15,17 +15,20 @@
 namespace snnk {
 namespace {
 
-// One thread per run of kImgP consecutive output pixels along x and group
+// One thread per run of P consecutive output pixels along x and group
 // of 8 output channels, channel group fastest: the 8 lanes of a pixel run
-// share its image reads (broadcast), each weight read from LDS feeds kImgP
+// share its image reads (broadcast), each weight read from LDS feeds P
 // FMAs, and a spike store of 8 lanes is one full 128-byte line.  The folded
 // weights of all output channels sit in LDS as [cin*9 + tap][Cout], staged
 // with every global read of a thread issued before its LDS writes (the
 // reads follow w's [Cout][K] order, so they coalesce).  Input channels go in
 // chunks of CC: a chunk's image reads (3 rows x (P+2) columns per channel)
 // are all issued before its FMAs, the first chunk's while the block stages
-// the weights.  Runs of P = 4 pixels need W % 4 == 0 and a grid that still
-// fills the GPU; otherwise runs are single pixels.
+// the weights.  Runs of P = 4 pixels (W % 4 == 0) while the grid still gives
+// every SIMD 1.5 waves, runs of 2 (W % 2 == 0) while it gives one, else
+// single pixels: at 32x32 images, B=32 takes 13.0 us with runs of 2 against
+// 13.8 us with runs of 4 (one wave per SIMD, nothing to hide its loads
+// behind), B=56 16.6 us with runs of 4 against 18.1 us with runs of 2.
 constexpr int kImgG = 8;
 constexpr int kImgMaxLds = 64 * 1024;
 
@@ -204,14 +207,19 @@ extern "C" int snnk_conv3x3_image_lif(const float* image, const float* w, const 
     return SNNK_EUNSUPPORTED;
   if (!aligned(spikes_out, 16)) return SNNK_EALIGN;
   const int64_t n_pix = B * H * W;
-  // runs of 4 pixels per thread when that still gives every CU a block
-  const int run = (W % 4 == 0 && n_pix / 4 * (Cout / kImgG) >= 256 * 256) ? 4 : 1;
+  // pixels per thread (see the kernel's comment); 256 * 256 threads are one
+  // wave per SIMD of the 256 CUs
+  const int64_t units = n_pix * (Cout / kImgG);
+  const int run = (W % 4 == 0 && units / 4 >= 3 * 256 * 128) ? 4
+                  : (W % 2 == 0 && units / 2 >= 256 * 256)   ? 2
+                                                               : 1;
   const int64_t blocks = (n_pix / run * (Cout / kImgG) + 255) / 256;
   if (blocks > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
   // channel chunk: 3 for RGB-like inputs, else 4
   const bool c3 = Cin % 3 == 0;
-  auto kern = run == 4 ? (c3 ? conv_image_lif_kernel<4, 3> : conv_image_lif_kernel<4, 4>)
-                       : (c3 ? conv_image_lif_kernel<1, 3> : conv_image_lif_kernel<1, 4>);
+  auto kern = run == 4   ? (c3 ? conv_image_lif_kernel<4, 3> : conv_image_lif_kernel<4, 4>)
+              : run == 2 ? (c3 ? conv_image_lif_kernel<2, 3> : conv_image_lif_kernel<2, 4>)
+                         : (c3 ? conv_image_lif_kernel<1, 3> : conv_image_lif_kernel<1, 4>);
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256),
                      static_cast<unsigned>(lds), static_cast<hipStream_t>(stream), image, w,
                      bias, spikes_out, static_cast<int>(T), static_cast<int>(n_pix),
