@@ -714,13 +714,27 @@ void auto_cfg_split(const ConvArgs& a, int* cfg, int* splits) {
     return;
   }
   if (rows > 1024 && rows <= 8192 && a.Cout <= 64) { *cfg = 4; return; }  // 32x128 would idle half
+  // M between the batch-32 and batch-56 VGG shapes (from a sweep at 56):
+  // the 8x8 layers take 128x128 tiles (with 2 K groups past K = 2048), the
+  // 4x4 layers 64x128 tiles (L9 at batch 56: 28.8 us against 52 us with the
+  // batch-32 fallback of 32x128 tiles and no split)
+  if (rows > 8192 && rows <= 16384 && a.Cout <= 512) { *cfg = K >= 2048 ? 9 : 11; return; }
+  if (rows > 2048 && rows <= 4096 && a.Cout <= 1024) {
+    if (K >= 4096) { *cfg = 3; *splits = 2; }                         // 64 x 128, 2 splits
+    else *cfg = 16;                                                   // 64 x 128, 4 stages
+    return;
+  }
   if (rows > 2048 || rows < 16) return;
   if (rows > 512) {
     if (K >= 4096) { *cfg = 3; *splits = 4; }                         // 64 x 128, 4 splits
-  } else if (rows > 128 && rows <= 256) {
-    if (K > 1024 && K <= 2048 && a.Cout <= 2048) { *cfg = 5; *splits = 2; }  // 32 x 128
+  } else if (rows > 128 && rows <= 256) {                             // FC layers at batch 56
+    if (a.Cout <= 64) { *cfg = 4; *splits = 4; }                      // 32 x 32
+    else if (K <= 512) { *cfg = 18; *splits = 1; }                    // 32 x 128, 2 K groups
+    else if (K > 2048) { *cfg = 3; *splits = 3; }                     // 64 x 128, 3 splits
+    else if (K > 1024 && a.Cout <= 2048) { *cfg = 13; *splits = 2; }  // 32 x 64
   } else if (rows <= 128) {
     if (a.Cout <= 64) { *cfg = 4; *splits = 4; }                      // 32 x 32
+    else if (rows <= 32) { *cfg = 4; *splits = 1; }                   // FC layers at batch 1
     else if (K > 2048 || (K > 1024 && a.Cout > 2048)) { *cfg = 13; *splits = 2; }  // 32 x 64
     else if (K > 1024) { *cfg = 4; *splits = 1; }  // 32 x 32, 4 K groups: 2x2 maps as Linear
   }
