@@ -688,7 +688,7 @@ int auto_cfg(const ConvArgs& a) {
   if (rows >= 32768) return a.Cout >= 256 ? 14 : (K <= 576 ? 3 : 9);
   if (rows >= 8192 && K <= 512) return a.Cout <= 512 ? 9 : 2;        // short K (SSA projections)
   if (rows >= 8192) return 3;                                         // 64 x 128
-  if (rows >= 2048) return 8;                                         // 32 x 128 split-K 4
+  if (rows >= 2048) return 18;                                        // 32 x 128 split-K 2
   if (rows >= 512) return 4;                                          // 32 x 32 split-K 4
   if (a.Cout <= 64) return 6;                                         // 32 x 32 split-K 8
   if (K <= 1024) return 7;                                            // 32 x 64 split-K 4
@@ -726,7 +726,7 @@ void auto_cfg_split(const ConvArgs& a, int* cfg, int* splits) {
   }
   if (rows > 2048 || rows < 16) return;
   if (rows > 512) {
-    if (K >= 4096) { *cfg = 3; *splits = 4; }                         // 64 x 128, 4 splits
+    if (K >= 4096) { *cfg = 10; *splits = 4; }                        // 128 x 64, 4 splits
   } else if (rows > 128 && rows <= 256) {                             // FC layers at batch 56
     if (a.Cout <= 64) { *cfg = 4; *splits = 4; }                      // 32 x 32
     else if (K <= 512) { *cfg = 18; *splits = 1; }                    // 32 x 128, 2 K groups
