@@ -41,11 +41,14 @@ def _flips_ok(got, ref, trace, pool, tol):
     return agree, bool(torch.any((got != ref) & ~near))
 
 
-@pytest.mark.parametrize("gain", [1.0, 3.0])
-def test_teacher_forced_layers(gain):
+@pytest.mark.parametrize("B,gain", [(32, 1.0), (32, 3.0), (1, 3.0), (56, 3.0)])
+def test_teacher_forced_layers(B, gain):
+    """Every layer fed the oracle's input; B = 1 and 56 run the plans chosen
+    for those batch sizes (32x32 tiles with K groups and splits at 1, larger
+    tiles and other splits at 56, the 2x2 layers as dense Linear at 32 and 56)."""
     eng = _engine(gain)
     params = ov.make_params(0, gain=gain)
-    img = _image(32)
+    img = _image(B)
     rec = ov.forward_layers(params, img, T)
     lif = eng._lif()
     convs = iter(eng.convs)
@@ -60,10 +63,14 @@ def test_teacher_forced_layers(gain):
         elif r["kind"] == "fc_lif":
             w, b = fcs.pop(0)
             x = r["input"]  # 1x1 spatial at 32x32: NCHW and NHWC flatten orders coincide
-            got = linear_bias_lif(x.to(DEV, torch.bfloat16).contiguous(), w, b, **lif).cpu().float()
+            R = (B + 3) // 4 * 4  # the kernel takes rows in fours, as the engine pads them
+            xp = torch.nn.functional.pad(x, (0, 0, 0, R - B))
+            got = linear_bias_lif(xp.to(DEV, torch.bfloat16).contiguous(), w, b, **lif)
+            got = got[:, :B].cpu().float()
         else:
-            y = linear_preact(r["input"].to(DEV, torch.bfloat16).contiguous(), eng.fc3_w,
-                              eng.fc3_b).cpu()[..., :10]
+            xp = torch.nn.functional.pad(r["input"], (0, 0, 0, (B + 3) // 4 * 4 - B))
+            y = linear_preact(xp.to(DEV, torch.bfloat16).contiguous(), eng.fc3_w,
+                              eng.fc3_b).cpu()[:, :B, :10]
             err = (y - r["output"]).abs().max().item()
             assert err < 5e-2, f"fc3 max err {err}"
             continue
