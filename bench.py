@@ -265,16 +265,10 @@ def bench_bgemm(args, dev):
                                                   out_dtype=torch.int32, out=Cs[i]),
                            nsets, args.steps, 2)
 
-    # one-off operand packing cost (activations would be packed per call)
+    # operand packing (activations would be packed per call), graph-timed:
+    # 8192x4096 uint8 {0,1} -> 8192x128 words, 37.7 MB of traffic per launch
     A_u8 = A.to(dev, torch.uint8)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(20):
-        snnk.pack_bits(A_u8, dim=-1)
-    e1.record()
-    torch.cuda.synchronize()
-    pack_ms = e0.elapsed_time(e1) / 20
+    _, pack_ms = time_gpu(lambda i: snnk.pack_bits(A_u8, dim=-1), 1, 20, 2)
 
     kinds = {"mfma_f4": ("bgemm_f4_kernel", FP4_PEAK_TOPS,
                          "dense MX fp4 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4)"),
@@ -300,6 +294,7 @@ def bench_bgemm(args, dev):
                     "achieved": other_tops, "peak": kinds[other][1],
                     "frac": other_tops / kinds[other][1]},
         "pack_A_ms": pack_ms,
+        "pack_A_tbps": (M * K + M * K // 8) / (pack_ms * 1e-3) / 1e12,
         "parity": bool(ok),
     }
     _with_traffic(rec["roofline"], "bgemm")
@@ -679,7 +674,8 @@ def main():
         "parity": head["parity"],
         "components": {n: {k: r[k] for k in ("value", "unit", "ms_per_step", "roofline",
                                              "parity", "cpu_baseline", "config", "compare",
-                                             "variants") if k in r}
+                                             "variants", "pack_A_ms", "pack_A_tbps", "spikes_packed")
+                           if k in r}
                        for n, r in recs.items() if n != names[0]},
     }
     print(json.dumps(out), flush=True)

@@ -33,6 +33,31 @@ def test_pack_bits_vs_oracle(dtype, shape, dim):
     assert got.shape == ref.shape and np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.uint8])
+@pytest.mark.parametrize("shape,dim", [((8, 4096), -1), ((5, 96), -1), ((3, 4, 160), -1),
+                                       ((6, 48), -1), ((2, 112), -1), ((70, 8), 0),
+                                       ((3, 100, 12), 1), ((64, 4096), 0)])
+def test_pack_bits_aligned_rows_any_values(dtype, shape, dim):
+    """Rows of 16-byte multiples packed along the last dim (one word per
+    thread) and 4-aligned rows packed along an outer dim (4 rows per
+    thread), with and without a partial last word: every nonzero element is
+    a 1 bit, whatever its value (uint8 0..255; -0.0 is zero, NaN nonzero)."""
+    g = torch.Generator().manual_seed(sum(shape))
+    if dtype == torch.uint8:
+        x = torch.randint(0, 256, shape, generator=g, dtype=torch.int32)
+        x = torch.where(torch.rand(shape, generator=g) < 0.5, torch.zeros_like(x), x).to(torch.uint8)
+    else:
+        x = torch.randn(shape, generator=g) * 1e-3
+        r = torch.rand(shape, generator=g)
+        x = torch.where(r < 0.4, torch.zeros_like(x), x)
+        x = torch.where((r >= 0.4) & (r < 0.5), torch.full_like(x, -0.0), x)
+        x = torch.where((r >= 0.5) & (r < 0.55), torch.full_like(x, float("nan")), x)
+        x = x.to(dtype)
+    got = snnk.pack_bits(x.to(DEV), dim=dim).cpu().numpy().view(np.uint32)
+    ref = ob.pack_axis((x != 0).to(torch.uint8).numpy(), dim % len(shape))
+    assert got.shape == ref.shape and np.array_equal(got, ref)
+
+
 def test_pack_known_answers():
     ones = torch.ones(1, 32, device=DEV)
     assert snnk.pack_bits(ones).cpu().numpy().view(np.uint32)[0, 0] == 0xFFFFFFFF

@@ -16,8 +16,9 @@ namespace snnk {
 namespace {
 
 // ---------------------------------------------------------------------------
-// pack: K contiguous (stride_k == 1).  One wave packs 64 consecutive elements
-// of one row per ballot; a wave walks 8 such chunks (512 elements).
+// pack: K contiguous (stride_k == 1) with rows that are not 16-byte aligned.
+// One wave packs 64 consecutive elements of one row per ballot; a wave walks
+// 8 such chunks (512 elements).
 // ---------------------------------------------------------------------------
 template <typename Raw>
 __device__ __forceinline__ bool nz(Raw v);
@@ -57,6 +58,73 @@ __global__ __launch_bounds__(256) void pack_contig_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// pack: K contiguous, rows 16-byte aligned.  One thread builds one word from
+// its 32 elements with 16-byte loads (2, 4 or 8 of them for 1-, 2- and
+// 4-byte elements); neighbouring threads take neighbouring words, so a
+// wave's loads cover one contiguous span and its word stores 256 contiguous
+// bytes.  The last word of a row with K % 32 != 0 reads element by element.
+// ---------------------------------------------------------------------------
+// Bit i of the result: element i of the 16 bytes in v is nonzero (the
+// element order of nz).
+template <typename Raw>
+__device__ __forceinline__ uint32_t nz_bits(u32x4 v);
+template <> __device__ __forceinline__ uint32_t nz_bits<uint8_t>(u32x4 v) {
+  uint32_t bits = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t d = v[i];
+    // bit 7 of each byte: the byte is nonzero ((b & 0x7F) + 0x7F carries
+    // into bit 7 unless the low seven bits are zero; the OR adds bit 7)
+    const uint32_t m = (((d & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | d) & 0x80808080u;
+    // bits 0, 8, 16, 24 -> bits 28..31 in byte order
+    bits |= (((m >> 7) * 0x10204080u) >> 28) << (4 * i);
+  }
+  return bits;
+}
+template <> __device__ __forceinline__ uint32_t nz_bits<uint16_t>(u32x4 v) {
+  uint32_t bits = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bits |= ((v[i] & 0x00007FFFu) != 0 ? 1u : 0u) << (2 * i);
+    bits |= ((v[i] & 0x7FFF0000u) != 0 ? 1u : 0u) << (2 * i + 1);
+  }
+  return bits;
+}
+template <> __device__ __forceinline__ uint32_t nz_bits<float>(u32x4 v) {
+  uint32_t bits = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bits |= ((v[i] & 0x7FFFFFFFu) != 0 ? 1u : 0u) << i;  // -0 is zero
+  return bits;
+}
+
+template <typename Raw>
+__global__ __launch_bounds__(256) void pack_word_kernel(
+    const Raw* __restrict__ src, uint32_t* __restrict__ dst, int64_t n_words, int64_t rows,
+    int64_t K, int64_t stride_b, int64_t stride_r, int64_t KW) {
+  constexpr int V = 16 / sizeof(Raw);  // elements per 16-byte load
+  constexpr int L = 32 / V;            // loads per word
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gid >= n_words) return;
+  const int64_t row = gid / KW, w = gid - row * KW;  // flattened (b, r), word
+  const int64_t b = row / rows, r = row - b * rows;
+  const Raw* s = src + b * stride_b + r * stride_r;
+  const int64_t k0 = w * 32;
+  uint32_t word = 0;
+  if (k0 + 32 <= K) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(s + k0);
+    u32x4 v[L];
+#pragma unroll
+    for (int i = 0; i < L; ++i) v[i] = __builtin_nontemporal_load(p + i);
+#pragma unroll
+    for (int i = 0; i < L; ++i) word |= nz_bits<Raw>(v[i]) << (i * V);
+  } else {
+    const int n = static_cast<int>(K - k0);
+    for (int j = 0; j < n; ++j) word |= (nz<Raw>(s[k0 + j]) ? 1u : 0u) << j;
+  }
+  dst[gid] = word;
+}
+
+// ---------------------------------------------------------------------------
 // pack: K strided.  One thread builds one word from 32 strided elements;
 // neighbouring threads take neighbouring rows so every read is coalesced
 // when stride_r == 1 (the reference's [TBH, N, D] -> [TBH, D, W] case).
@@ -80,18 +148,87 @@ __global__ __launch_bounds__(256) void pack_strided_kernel(
   dst[(b * rows + r) * KW + w] = word;
 }
 
+// ---------------------------------------------------------------------------
+// pack: K strided over contiguous rows (stride_r == 1, rows % 4 == 0, every
+// 4-row group aligned).  A thread builds the words of 4 adjacent rows with
+// one 4-element load per k (4, 8 or 16 bytes), neighbouring threads on
+// neighbouring row groups, so a wave's load covers one contiguous span.
+// ---------------------------------------------------------------------------
+template <typename Raw> struct Quad;
+template <> struct Quad<uint8_t> { typedef uint32_t type; };
+template <> struct Quad<uint16_t> { typedef u32x2 type; };
+template <> struct Quad<float> { typedef u32x4 type; };
+
+// bit i (i < 4): element i of the 4 loaded is nonzero
+__device__ __forceinline__ uint32_t nz4(uint32_t v) {  // 4 bytes
+  const uint32_t m = (((v & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | v) & 0x80808080u;
+  return ((m >> 7) * 0x10204080u) >> 28;
+}
+__device__ __forceinline__ uint32_t nz4(u32x2 v) {  // 4 x 16-bit
+  return ((v[0] & 0x7FFFu) != 0 ? 1u : 0u) | ((v[0] & 0x7FFF0000u) != 0 ? 2u : 0u) |
+         ((v[1] & 0x7FFFu) != 0 ? 4u : 0u) | ((v[1] & 0x7FFF0000u) != 0 ? 8u : 0u);
+}
+__device__ __forceinline__ uint32_t nz4(u32x4 v) {  // 4 x fp32
+  return ((v[0] & 0x7FFFFFFFu) != 0 ? 1u : 0u) | ((v[1] & 0x7FFFFFFFu) != 0 ? 2u : 0u) |
+         ((v[2] & 0x7FFFFFFFu) != 0 ? 4u : 0u) | ((v[3] & 0x7FFFFFFFu) != 0 ? 8u : 0u);
+}
+
+template <typename Raw>
+__global__ __launch_bounds__(256) void pack_strided4_kernel(
+    const Raw* __restrict__ src, uint32_t* __restrict__ dst, int64_t batch, int64_t rows,
+    int64_t K, int64_t stride_b, int64_t stride_k, int64_t KW) {
+  typedef typename Quad<Raw>::type Q;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t rq = rows / 4;
+  const int64_t per_b = KW * rq;  // thread order: (b, w, row group) with the group fastest
+  if (tid >= batch * per_b) return;
+  const int64_t b = tid / per_b;
+  const int64_t rem = tid - b * per_b;
+  const int64_t w = rem / rq, r0 = (rem - w * rq) * 4;
+  const Raw* s = src + b * stride_b + r0;
+  const int64_t k0 = w * 32;
+  const int n = static_cast<int>((K - k0) < 32 ? (K - k0) : 32);
+  uint32_t word[4] = {0u, 0u, 0u, 0u};
+#pragma unroll 8
+  for (int j = 0; j < n; ++j) {
+    const uint32_t q = nz4(__builtin_nontemporal_load(reinterpret_cast<const Q*>(s + (k0 + j) * stride_k)));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) word[i] |= ((q >> i) & 1u) << j;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[(b * rows + r0 + i) * KW + w] = word[i];
+}
+
 template <typename Raw>
 int launch_pack(const void* src, uint32_t* dst, int64_t batch, int64_t rows, int64_t K,
                 int64_t sb, int64_t sr, int64_t sk, hipStream_t stream) {
   const int64_t KW = (K + 31) / 32;
   const Raw* s = static_cast<const Raw*>(src);
-  if (sk == 1) {
+  const int64_t eb = static_cast<int64_t>(sizeof(Raw));
+  // every row starts on a 16-byte boundary (a stride of a dimension of
+  // extent 1 is never applied)
+  const bool rows_aligned = aligned(s, 16) && (rows == 1 || ((sr * eb) & 15) == 0) &&
+                            (batch == 1 || ((sb * eb) & 15) == 0);
+  if (sk == 1 && rows_aligned) {
+    const int64_t n_words = batch * rows * KW;
+    const int64_t blocks = (n_words + 255) / 256;
+    if (blocks > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
+    hipLaunchKernelGGL(pack_word_kernel<Raw>, dim3(blocks), dim3(256), 0, stream,
+                       s, dst, n_words, rows, K, sb, sr, KW);
+  } else if (sk == 1) {
     const int64_t cpr = (K + 64 * kPackChunks - 1) / (64 * kPackChunks);
     const int64_t waves = batch * rows * cpr;
     const int64_t blocks = (waves + 3) / 4;
     if (blocks > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
     hipLaunchKernelGGL(pack_contig_kernel<Raw>, dim3(blocks), dim3(256), 0, stream,
                        s, dst, batch, rows, K, sb, sr, KW);
+  } else if (sr == 1 && rows % 4 == 0 && aligned(s, 4 * eb) && ((sk * eb) % (4 * eb)) == 0 &&
+             (batch == 1 || ((sb * eb) % (4 * eb)) == 0)) {
+    const int64_t threads = batch * (rows / 4) * KW;
+    const int64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
+    hipLaunchKernelGGL(pack_strided4_kernel<Raw>, dim3(blocks), dim3(256), 0, stream,
+                       s, dst, batch, rows, K, sb, sk, KW);
   } else {
     const int64_t threads = batch * rows * KW;
     const int64_t blocks = (threads + 255) / 256;
