@@ -130,9 +130,15 @@ __device__ __forceinline__ uint32_t channel_of(const LifArgs& a, uint64_t i) {
   return static_cast<uint32_t>(q % a.C64);
 }
 
+// v of another lane of the same 16-lane row (DPP control CTRL)
+template <int CTRL>
+__device__ __forceinline__ uint32_t lane_dpp(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
 // Tag: input element type; SPK: 0 = spikes in the input type, 1 = uint8,
 // 2 = bf16, 3 = packed bits (a lane's VEC spike bits are OR-combined across
-// the 32/VEC lanes of one 32-neuron word by xor shuffles; NCL % 32 == 0 makes
+// the 32/VEC lanes of one 32-neuron word by DPP lane exchanges; NCL % 32 == 0 makes
 // every word's lanes all active or all retired);
 // VEC: neurons per thread (VEC == 1 is the unaligned / ragged fallback).
 template <typename Tag, int SPK, int VEC, bool HAS_RES>
@@ -196,8 +202,14 @@ __global__ __launch_bounds__(kBlock) void lif_kernel(LifArgs a) {
         if constexpr (SPK == 3) {
           const int lane = threadIdx.x & 63;
           uint32_t w = nib << (VEC * (lane % kLanesPerWord));
-#pragma unroll
-          for (int m = 1; m < kLanesPerWord; m <<= 1) w |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), m));
+          // OR over the word's lanes: DPP within a 16-lane row (lane ^ 1,
+          // lane ^ 2, then the mirror lane of the other half of 8), a
+          // shuffle beyond it; every lane of the group ends with the word
+          if constexpr (kLanesPerWord >= 2) w |= lane_dpp<0xB1>(w);   // quad_perm [1,0,3,2]
+          if constexpr (kLanesPerWord >= 4) w |= lane_dpp<0x4E>(w);   // quad_perm [2,3,0,1]
+          if constexpr (kLanesPerWord >= 8) w |= lane_dpp<0x141>(w);  // row_half_mirror
+          if constexpr (kLanesPerWord >= 16) w |= lane_dpp<0x140>(w); // row_mirror
+          if constexpr (kLanesPerWord >= 32) w |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), 16));
           if (s_out && lane % kLanesPerWord == 0) {
             const uint64_t off = static_cast<uint64_t>(t0 + k) * (ncl / 32) + i0 / 32;
             reinterpret_cast<uint32_t*>(a.spikes)[off] = w;
