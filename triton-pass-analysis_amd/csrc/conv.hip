@@ -144,6 +144,12 @@ struct Cfg {
 
 __device__ __forceinline__ uint16_t spike_bf16(bool s) { return s ? 0x3F80u : 0u; }
 
+// v of the lane CTRL names within each group of 4 lanes (DPP quad_perm)
+template <int CTRL>
+__device__ __forceinline__ uint32_t quad_dpp(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
 // TAPS = 9: 3x3 conv, pad 1.  TAPS = 1: 1x1 conv, i.e. a Linear layer over
 // the rows of [T][rows][Cin] (H = 1, W = rows).
 template <int TAPS>
@@ -322,13 +328,14 @@ void conv3x3_kernel(ConvArgs a) {
             any = any || s;
           }
           if constexpr (kColPool) {
-            // lanes 4k..4k+3 hold adjacent columns of the same rows
+            // lanes 4k..4k+3 hold adjacent columns of the same rows: OR the
+            // 4 pixels' spikes (bit q) over the quad with two DPP exchanges
+            uint32_t m = (sp[0] ? 1u : 0u) | (sp[1] ? 2u : 0u) | (sp[2] ? 4u : 0u) | (sp[3] ? 8u : 0u);
+            m |= quad_dpp<0xB1>(m);  // lane ^ 1
+            m |= quad_dpp<0x4E>(m);  // lane ^ 2
+            if ((r_lane & 3) == 0) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              int sq = sp[q] ? 1 : 0;
-              sq |= __shfl_xor(sq, 1, 64);
-              sq |= __shfl_xor(sq, 2, 64);
-              if ((r_lane & 3) == 0) o[q * o_cols] = spike_bf16(sq != 0);
+              for (int q = 0; q < 4; ++q) o[q * o_cols] = spike_bf16(((m >> q) & 1u) != 0);
             }
           } else if constexpr (POOL) {
             o[0] = spike_bf16(any);
