@@ -107,6 +107,7 @@ struct ConvArgs {
   uint32_t w_bytes;      // bytes of w, at most kFar
   int64_t o_tstride;     // B*Ho*Wo*Cout
   int tiles_m, tiles_n;  // output tiles along rows (quads) and Cout
+  FastDiv div_tiles_m, div_tiles_n;
   // cross-block split-K: `splits` blocks share one output tile, each over
   // `stages_per_split` K stages; partial sums go to `partials`, the last
   // block of a tile (ticket in `tickets`) reduces them in split order
@@ -180,15 +181,17 @@ void conv3x3_kernel(ConvArgs a) {
   const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (tile >= n_tiles) return;  // whole workgroup: no barrier is left waiting
   int tm, tn, split;
+  // (multiply-high dividers: a runtime integer division is ~30 instructions
+  // of straight-line code, fetched cold at the start of every launch)
   if (a.splits == 1) {
-    tm = tile / a.tiles_n;
+    tm = static_cast<int>(fdiv(static_cast<uint32_t>(tile), a.div_tiles_n));
     tn = tile - tm * a.tiles_n;
     split = 0;
   } else {
-    tm = tile % a.tiles_m;
-    const int rest = tile / a.tiles_m;
-    tn = rest % a.tiles_n;
-    split = rest / a.tiles_n;
+    const int rest = static_cast<int>(fdiv(static_cast<uint32_t>(tile), a.div_tiles_m));
+    tm = tile - rest * a.tiles_m;
+    split = static_cast<int>(fdiv(static_cast<uint32_t>(rest), a.div_tiles_n));
+    tn = rest - split * a.tiles_n;
   }
   const int mn = tm * a.tiles_n + tn;  // output tile id
   const int quad0 = tm * C::kQuads;
@@ -797,6 +800,8 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
   ConvArgs a = a0;
   a.tiles_m = p.tiles_m;
   a.tiles_n = p.tiles_n;
+  a.div_tiles_m = make_fastdiv(static_cast<uint32_t>(std::max(1, p.tiles_m)));
+  a.div_tiles_n = make_fastdiv(static_cast<uint32_t>(std::max(1, p.tiles_n)));
   a.splits = p.splits;
   a.stages_per_split = p.stages_per_split;
   a.tickets = static_cast<unsigned int*>(workspace);
