@@ -265,6 +265,19 @@ def bench_bgemm(args, dev):
                                                   out_dtype=torch.int32, out=Cs[i]),
                            nsets, args.steps, 2)
 
+    # BASELINE's signed-weight variant (W in {-1,+1}: 2*popc(A & W+) - popc(A))
+    # on the same operands and kernel; exact row sample and checksums again
+    _, signed_ms = time_gpu(lambda i: _gemm_packed(As[i], Ws[i], K, signed=True, algo=algo,
+                                                   out_dtype=torch.int32, out=Cs[i]),
+                            nsets, args.steps, 2)
+    Cs_np = Cs[0].cpu().numpy().astype(np.int64)
+    A64, W64 = A_np.astype(np.int64), W_np.astype(np.int64)
+    rowpop = A64.sum(1)
+    ok_signed = np.array_equal(Cs_np[:64], 2 * Cn[:64] - rowpop[:64, None])
+    ok_signed = ok_signed and np.array_equal(Cs_np.sum(1), 2 * (A64 @ W64.sum(1)) - N * rowpop)
+    ok_signed = ok_signed and np.array_equal(Cs_np.sum(0), 2 * (A64.sum(0) @ W64) - rowpop.sum())
+    signed_tops = ops / (signed_ms * 1e-3) / 1e12
+
     # operand packing (activations would be packed per call), graph-timed:
     # 8192x4096 uint8 {0,1} -> 8192x128 words, 37.7 MB of traffic per launch
     A_u8 = A.to(dev, torch.uint8)
@@ -293,9 +306,12 @@ def bench_bgemm(args, dev):
         "compare": {"algo": other, "kernel": kinds[other][0], "kernel_ms_mean": other_ms,
                     "achieved": other_tops, "peak": kinds[other][1],
                     "frac": other_tops / kinds[other][1]},
+        "variants": {"signed_weights": {"kernel_ms_mean": signed_ms, "achieved": signed_tops,
+                                        "unit": "TOPS", "frac": signed_tops / peak,
+                                        "parity": bool(ok_signed)}},
         "pack_A_ms": pack_ms,
         "pack_A_tbps": (M * K + M * K // 8) / (pack_ms * 1e-3) / 1e12,
-        "parity": bool(ok),
+        "parity": bool(ok and ok_signed),
     }
     _with_traffic(rec["roofline"], "bgemm")
     if not args.no_cpu_baseline:
