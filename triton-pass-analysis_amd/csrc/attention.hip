@@ -39,6 +39,7 @@ struct AttnArgs {
   int T, B, H, N, d;
   float decay, in_scale, vth, v_reset;
   int soft_reset;
+  int o_vec;  // output rows and steps 8-byte aligned: 4 spikes per store
 };
 
 // Two words of bf16 pairs (4 elements) -> 4 bytes, 1 where the element is nonzero.
@@ -48,11 +49,20 @@ __device__ __forceinline__ uint32_t bytes4(uint32_t lo, uint32_t hi) {
   return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
 }
 
-// Block = 4 waves for one (batch, head).  Staging is shared by the 256
-// threads; wave w computes S tile (w / NT, w % NT) when w < NT*NT and owns
-// O tile (w / DT, w % DT) -- with its LIF membrane -- when w < NT*DT.
+// Block = 8 waves for one (batch, head).  Each of the 512 threads stages one
+// 8-dim chunk of Q_t and of K_t and a 4-token x 2-dim patch of V_t; wave w
+// computes S tile (w / NT, w % NT) when w < NT*NT and owns O tile
+// (w / DT, w % DT) -- with its LIF membrane -- when w < NT*DT.  Both products
+// are formed transposed (S^T = K Q^T, O^T = V^T S^T: the MFMA operands
+// swapped) so that a lane's accumulator holds 4 consecutive columns of S and
+// of O: one 4-byte LDS write per 4 entries of S and one 8-byte store per 4
+// spikes of the output.
+constexpr int kThreads = 512;
+static_assert(kMaxTok * (kMaxDim / 8) == kThreads, "one Q/K chunk per thread");
+static_assert((kMaxTok / 4) * (kMaxDim / 2) == kThreads, "one V patch per thread");
+
 template <int NT, int DT>  // token tiles, dim tiles (32 each)
-__global__ __launch_bounds__(256) void ssa_attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kThreads) void ssa_attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t qs[kMaxTok * kPitch];
   __shared__ __attribute__((aligned(16))) int8_t ks[kMaxTok * kPitch];
   __shared__ __attribute__((aligned(16))) int8_t vt[kMaxDim * kPitch];  // [dim][token]
@@ -73,50 +83,52 @@ __global__ __launch_bounds__(256) void ssa_attention_kernel(AttnArgs a) {
   const int si = wave / NT, sj = wave % NT;
   const bool has_o = wave < NT * DT;
   const int oi = wave / DT, od = wave % DT;
-  const int dd = od * 32 + r32;
-  uint16_t* ob = a.out + row0 * a.o_row + h * a.d + dd;
+  // O^T accumulator of this lane: token oi*32 + r32, dims od*32 + 8*(e/4) + 4*g + e%4
+  const int ti = oi * 32 + r32;
+  uint16_t* ob = a.out + (row0 + ti) * a.o_row + h * a.d;
   float vm[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) vm[e] = 0.0f;
 
   // ---- staging of Q_t, K_t (row = token) and V_t^T (row = dim) as int8 ----
-  // 64 tokens x 8 chunks of 8 dims per tensor; consecutive threads walk along
-  // a token row with 16-byte loads; padding rows / dims are zeros.  The loads
-  // of step t+1 are issued into registers before step t's MFMAs, so only the
-  // first step waits for memory.
-  u32x4 rq[2], rk[2], rv[2];
+  // Q/K: thread = (token n, chunk c of 8 dims), one 16-byte load each.
+  // V: thread = (4 tokens from 4*n4, dims 2p and 2p+1), four 4-byte loads that
+  // become one 4-byte row segment of V^T per dim.  Padding tokens and dims
+  // are zeros.  The loads of step t+1 are issued into registers before step
+  // t's MFMAs, so only the first step waits for memory.
+  const int qn = tid >> 3, qc = tid & 7;
+  const int vp = tid & 31, vn4 = tid >> 5;
+  const bool q_in = qn < a.N && qc * 8 < a.d;
+  const bool v_in = 2 * vp < a.d;
+  u32x4 rq, rk;
+  uint32_t rv[4];
   auto load_step = [&](int t) {
-    const uint16_t* qt = qb + t * a.q_t;
-    const uint16_t* kt = kb + t * a.k_t;
-    const uint16_t* vtp = vb + t * a.v_t;
+    rq = rk = u32x4{0u, 0u, 0u, 0u};
+    if (q_in) {
+      rq = *reinterpret_cast<const u32x4*>(qb + t * a.q_t + qn * a.q_row + qc * 8);
+      rk = *reinterpret_cast<const u32x4*>(kb + t * a.k_t + qn * a.k_row + qc * 8);
+    }
+    const uint16_t* vtp = vb + t * a.v_t + 2 * vp;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int ci = tid + 256 * m;
-      const int n = ci >> 3, c = ci & 7;
-      rq[m] = rk[m] = rv[m] = u32x4{0u, 0u, 0u, 0u};
-      if (n < a.N && c * 8 < a.d) {
-        rq[m] = *reinterpret_cast<const u32x4*>(qt + n * a.q_row + c * 8);
-        rk[m] = *reinterpret_cast<const u32x4*>(kt + n * a.k_row + c * 8);
-        rv[m] = *reinterpret_cast<const u32x4*>(vtp + n * a.v_row + c * 8);
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int n = 4 * vn4 + u;
+      rv[u] = (v_in && n < a.N) ? *reinterpret_cast<const uint32_t*>(vtp + n * a.v_row) : 0u;
     }
   };
   auto store_step = [&]() {
+    u32x2 bq, bk;
+    bq[0] = bytes4(rq[0], rq[1]); bq[1] = bytes4(rq[2], rq[3]);
+    bk[0] = bytes4(rk[0], rk[1]); bk[1] = bytes4(rk[2], rk[3]);
+    *reinterpret_cast<u32x2*>(qs + qn * kPitch + qc * 8) = bq;
+    *reinterpret_cast<u32x2*>(ks + qn * kPitch + qc * 8) = bk;
+    uint32_t lo = 0u, hi = 0u;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int ci = tid + 256 * m;
-      const int n = ci >> 3, c = ci & 7;
-      u32x2 bq, bk;
-      bq[0] = bytes4(rq[m][0], rq[m][1]); bq[1] = bytes4(rq[m][2], rq[m][3]);
-      bk[0] = bytes4(rk[m][0], rk[m][1]); bk[1] = bytes4(rk[m][2], rk[m][3]);
-      *reinterpret_cast<u32x2*>(qs + n * kPitch + c * 8) = bq;
-      *reinterpret_cast<u32x2*>(ks + n * kPitch + c * 8) = bk;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t w = rv[m][e >> 1] >> (16 * (e & 1));
-        vt[(c * 8 + e) * kPitch + n] = (w & 0x7FFFu) ? 1 : 0;
-      }
+    for (int u = 0; u < 4; ++u) {
+      lo |= ((rv[u] & 0x7FFFu) ? 1u : 0u) << (8 * u);
+      hi |= ((rv[u] & 0x7FFF0000u) ? 1u : 0u) << (8 * u);
     }
+    *reinterpret_cast<uint32_t*>(vt + (2 * vp) * kPitch + 4 * vn4) = lo;
+    *reinterpret_cast<uint32_t*>(vt + (2 * vp + 1) * kPitch + 4 * vn4) = hi;
   };
 
   load_step(0);
@@ -125,61 +137,79 @@ __global__ __launch_bounds__(256) void ssa_attention_kernel(AttnArgs a) {
     __syncthreads();
     if (t + 1 < a.T) load_step(t + 1);
 
-    // ---- S = Q K^T (one 32x32 tile per wave) --------------------------------
+    // ---- S^T = K Q^T (one 32x32 tile per wave) ------------------------------
     if (has_s) {
       i32x16 acc;
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[e] = 0;
 #pragma unroll
       for (int kk = 0; kk < kMaxDim / 32; ++kk) {
-        const i32x4 fa = *reinterpret_cast<const i32x4*>(qs + (si * 32 + r32) * kPitch + kk * 32 + g * 16);
-        const i32x4 fb = *reinterpret_cast<const i32x4*>(ks + (sj * 32 + r32) * kPitch + kk * 32 + g * 16);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, acc, 0, 0, 0);
+        const i32x4 fk = *reinterpret_cast<const i32x4*>(ks + (sj * 32 + r32) * kPitch + kk * 32 + g * 16);
+        const i32x4 fq = *reinterpret_cast<const i32x4*>(qs + (si * 32 + r32) * kPitch + kk * 32 + g * 16);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fk, fq, acc, 0, 0, 0);
       }
-      // register e of lane l: row 8*(e/4) + 4*g + e%4, column l%32
-      const int j = sj * 32 + r32;
+      // register e of lane l: S[i][j] with i = si*32 + l%32 (query) and
+      // j = sj*32 + 8*(e/4) + 4*g + e%4 (key): 4 consecutive j per e/4
+      const int i = si * 32 + r32;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int i = si * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-        ss[i * kPitch + j] = static_cast<int8_t>(acc[e]);
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const uint32_t w = (static_cast<uint32_t>(acc[4 * e4]) & 0xFFu) |
+                           ((static_cast<uint32_t>(acc[4 * e4 + 1]) & 0xFFu) << 8) |
+                           ((static_cast<uint32_t>(acc[4 * e4 + 2]) & 0xFFu) << 16) |
+                           (static_cast<uint32_t>(acc[4 * e4 + 3]) << 24);
+        *reinterpret_cast<uint32_t*>(ss + i * kPitch + sj * 32 + 8 * e4 + 4 * g) = w;
       }
       if (a.s_counts) {
         int32_t* sc = a.s_counts + ((static_cast<int64_t>(t) * a.B * a.H + bh) * a.N) * a.N;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int i = si * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+          const int j = sj * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
           if (i < a.N && j < a.N) sc[i * a.N + j] = acc[e];
         }
       }
     }
     __syncthreads();
 
-    // ---- O = S V and the LIF (one 32x32 tile per wave) --------------------------
+    // ---- O^T = V^T S^T and the LIF (one 32x32 tile per wave) -------------------
     if (has_o) {
       i32x16 acc;
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[e] = 0;
 #pragma unroll
       for (int kk = 0; kk < NT; ++kk) {
-        const i32x4 fa = *reinterpret_cast<const i32x4*>(ss + (oi * 32 + r32) * kPitch + kk * 32 + g * 16);
-        const i32x4 fb = *reinterpret_cast<const i32x4*>(vt + (od * 32 + r32) * kPitch + kk * 32 + g * 16);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, acc, 0, 0, 0);
+        const i32x4 fv = *reinterpret_cast<const i32x4*>(vt + (od * 32 + r32) * kPitch + kk * 32 + g * 16);
+        const i32x4 fs = *reinterpret_cast<const i32x4*>(ss + (oi * 32 + r32) * kPitch + kk * 32 + g * 16);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fv, fs, acc, 0, 0, 0);
       }
       uint16_t* ot = ob + t * a.o_t;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int i = oi * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-        const float hm = __fadd_rn(__fmul_rn(a.decay, vm[e]), __fmul_rn(a.in_scale, static_cast<float>(acc[e])));
-        const bool sp = hm >= a.vth;
-        vm[e] = sp ? (a.soft_reset ? __fsub_rn(hm, a.vth) : a.v_reset) : hm;
-        if (i < a.N && dd < a.d) ot[i * a.o_row] = sp ? 0x3F80u : 0u;
+      for (int e4 = 0; e4 < 4; ++e4) {
+        uint32_t spk[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = 4 * e4 + u;
+          const float hm = __fadd_rn(__fmul_rn(a.decay, vm[e]), __fmul_rn(a.in_scale, static_cast<float>(acc[e])));
+          const bool sp = hm >= a.vth;
+          vm[e] = sp ? (a.soft_reset ? __fsub_rn(hm, a.vth) : a.v_reset) : hm;
+          spk[u] = sp ? 0x3F80u : 0u;
+        }
+        // 4 dims from dd0; d % 8 == 0, so they are all in range when dd0 is
+        const int dd0 = od * 32 + 8 * e4 + 4 * g;
+        if (ti < a.N && dd0 < a.d) {
+          if (a.o_vec) {
+            *reinterpret_cast<u32x2*>(ot + dd0) = u32x2{spk[0] | (spk[1] << 16), spk[2] | (spk[3] << 16)};
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) ot[dd0 + u] = static_cast<uint16_t>(spk[u]);
+          }
+        }
       }
       if (a.o_counts) {
         int32_t* oc = a.o_counts + ((static_cast<int64_t>(t) * a.B * a.H + bh) * a.N) * a.d;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int i = oi * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-          if (i < a.N && dd < a.d) oc[i * a.d + dd] = acc[e];
+          const int dd = od * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+          if (ti < a.N && dd < a.d) oc[ti * a.d + dd] = acc[e];
         }
       }
     }
@@ -220,11 +250,12 @@ extern "C" int snnk_spike_attention(const uint16_t* q, const uint16_t* k, const 
   a.N = static_cast<int>(N); a.d = static_cast<int>(d);
   a.decay = decay; a.in_scale = in_scale; a.vth = v_threshold; a.v_reset = v_reset;
   a.soft_reset = soft_reset ? 1 : 0;
+  a.o_vec = aligned(spikes_out, 8) && out_row % 4 == 0 && out_step % 4 == 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nt = N > 32 ? 2 : 1, dt = d > 32 ? 2 : 1;
-  if (nt == 1 && dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 1>), dim3(B * H), dim3(256), 0, s, a);
-  else if (nt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 2>), dim3(B * H), dim3(256), 0, s, a);
-  else if (dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<2, 1>), dim3(B * H), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((ssa_attention_kernel<2, 2>), dim3(B * H), dim3(256), 0, s, a);
+  if (nt == 1 && dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 1>), dim3(B * H), dim3(kThreads), 0, s, a);
+  else if (nt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 2>), dim3(B * H), dim3(kThreads), 0, s, a);
+  else if (dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<2, 1>), dim3(B * H), dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL((ssa_attention_kernel<2, 2>), dim3(B * H), dim3(kThreads), 0, s, a);
   return launch_status();
 }
