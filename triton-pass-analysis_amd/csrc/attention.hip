@@ -40,6 +40,7 @@ struct AttnArgs {
   float decay, in_scale, vth, v_reset;
   int soft_reset;
   int o_vec;  // output rows and steps 8-byte aligned: 4 spikes per store
+  int per_xcd;  // (batch, head) blocks per XCD
 };
 
 // Two words of bf16 pairs (4 elements) -> 4 bytes, 1 where the element is nonzero.
@@ -70,7 +71,13 @@ __global__ __launch_bounds__(kThreads) void ssa_attention_kernel(AttnArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int bh = blockIdx.x;
+  // Workgroups are dealt to the 8 XCDs round-robin by id; id -> (batch, head)
+  // is remapped so that each XCD runs a contiguous range of heads.  The heads
+  // of one batch then share an XCD's L2, which fetches each 128-byte line of
+  // their token rows once (a head's d columns straddle lines that the
+  // neighbouring heads also read).
+  const int bh = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
+  if (bh >= a.B * a.H) return;
   const int b = bh / a.H, h = bh - b * a.H;
   const int r32 = lane & 31, g = lane >> 5;
   // this block's (batch, head) slice: token row 0, column h*d
@@ -251,11 +258,13 @@ extern "C" int snnk_spike_attention(const uint16_t* q, const uint16_t* k, const 
   a.decay = decay; a.in_scale = in_scale; a.vth = v_threshold; a.v_reset = v_reset;
   a.soft_reset = soft_reset ? 1 : 0;
   a.o_vec = aligned(spikes_out, 8) && out_row % 4 == 0 && out_step % 4 == 0;
+  a.per_xcd = static_cast<int>((B * H + 7) / 8);
+  const dim3 grid(static_cast<unsigned>(a.per_xcd) * 8u);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nt = N > 32 ? 2 : 1, dt = d > 32 ? 2 : 1;
-  if (nt == 1 && dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 1>), dim3(B * H), dim3(kThreads), 0, s, a);
-  else if (nt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 2>), dim3(B * H), dim3(kThreads), 0, s, a);
-  else if (dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<2, 1>), dim3(B * H), dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL((ssa_attention_kernel<2, 2>), dim3(B * H), dim3(kThreads), 0, s, a);
+  if (nt == 1 && dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 1>), grid, dim3(kThreads), 0, s, a);
+  else if (nt == 1) hipLaunchKernelGGL((ssa_attention_kernel<1, 2>), grid, dim3(kThreads), 0, s, a);
+  else if (dt == 1) hipLaunchKernelGGL((ssa_attention_kernel<2, 1>), grid, dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL((ssa_attention_kernel<2, 2>), grid, dim3(kThreads), 0, s, a);
   return launch_status();
 }
