@@ -275,7 +275,8 @@ int snnk_linear_mean_t(const uint16_t* x, const uint16_t* w, const float* bias, 
  * q, k, v: bf16 spikes; element (t, token row r = b*N + n, head h, dim dd) at
  *   ptr + t*step + r*row + h*d + dd (q/k/v may be column slices of one
  *   [T][B*N][3*H*d] projection output).  N <= 64 tokens, d <= 64,
- *   d % 8 == 0; pointers 16-byte aligned, row and step strides multiples of 8.
+ *   d % 8 == 0; pointers 16-byte aligned, row and step strides multiples of 8,
+ *   row strides below 2^23 elements (SNNK_EUNSUPPORTED otherwise).
  * spikes_out: bf16, element (t, r, h*d + dd) at out + t*out_step + r*out_row + h*d + dd.
  * s_counts: NULL or int32 [T][B][H][N][N] (Q K^T); o_counts: NULL or int32
  *   [T][B][H][N][d] ((Q K^T) V).
