@@ -65,3 +65,34 @@ def test_workspace_size_queries_without_gpu():
     lin = _abi.lib().snnk_linear_bias_lif_ws_size
     assert lin(4, 32, 4096, 4096, 0, -1, 1) == 0 and lin(4, 32, 4096, 4096, 0, -1, 0) > 0
     assert _abi.lib().snnk_status_string(_abi.EWORKSPACE) == b"workspace missing or too small"
+
+
+def test_workspace_pool_keys_by_device_and_stream():
+    """Split-K calls on two streams must not share a workspace: the pool hands
+    each (device, stream) its own buffer, grows one without touching the
+    others, and refuses to grow during graph capture."""
+    import pytest
+    import torch
+    from snnk._workspace import WorkspacePool
+
+    made = []
+
+    def alloc(dev, nbytes):
+        made.append((dev, nbytes))
+        return torch.zeros(nbytes, dtype=torch.uint8)
+
+    pool = WorkspacePool(alloc=alloc, min_bytes=1 << 20)
+    a = pool.get(0, 0x1000, 100)
+    b = pool.get(0, 0x2000, 100)
+    c = pool.get(1, 0x1000, 100)
+    assert a is not b and a is not c and b is not c
+    assert pool.get(0, 0x1000, 5000) is a                 # fits: reused
+    assert pool.get(0, 0x1000, 0) is None
+    big = pool.get(0, 0x1000, 3 << 20)                    # grows this stream only
+    assert big is not a and big.numel() == 3 << 20
+    assert pool.get(0, 0x2000, 100) is b
+    assert len(made) == 4
+    with pytest.raises(RuntimeError, match="capture"):
+        pool.get(0, 0x3000, 100, capturing=True)          # new stream inside a capture
+    assert pool.get(0, 0x2000, 100, capturing=True) is b  # existing buffer is fine
+

@@ -46,6 +46,34 @@ def test_attention_core_counts_and_spikes_exact(T, B, H, N, d):
     assert torch.equal(got, a_ref)
 
 
+@pytest.mark.parametrize("T,B,H,N,d,soft,v_reset", [
+    (3, 2, 2, 20, 48, True, 0.0),     # one token tile, two dim tiles, soft reset
+    (4, 2, 2, 20, 48, False, 0.25),   # same tiling, hard reset to a non-zero value
+    (2, 3, 2, 32, 64, True, 0.0),     # N = 32 exactly, d = 64
+    (4, 1, 3, 17, 40, False, -0.5),   # ragged N and d, negative reset value
+    (5, 2, 1, 50, 24, True, 0.0),     # two token tiles, one dim tile, soft reset
+])
+def test_attention_core_reset_modes_exact(T, B, H, N, d, soft, v_reset):
+    """Every reset template of the core against oracle lif_multistep; with the
+    power-of-two scale every membrane value is exact in fp32."""
+    D = H * d
+    qkv = _spikes((T, B * N, 3 * D), 0.3, 1000 + N * d)
+    qd = qkv.to(DEV, torch.bfloat16)
+    q, k, v = qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:]
+    spk, S, O = spike_attention(q, k, v, B=B, N=N, heads=H, scale=0.125, tau=2.0,
+                                v_threshold=0.5, v_reset=v_reset, soft_reset=soft,
+                                return_counts=True)
+    hq = lambda s: s.view(T, B, N, H, d).permute(0, 1, 3, 2, 4).long()  # noqa: E731
+    qh, kh, vh = hq(qkv[..., :D]), hq(qkv[..., D:2 * D]), hq(qkv[..., 2 * D:])
+    O_ref = (qh @ kh.transpose(-1, -2)) @ vh
+    assert torch.equal(O.cpu().long(), O_ref)
+    a_ref, _, _ = on.lif_multistep(O_ref.float() * 0.125, neuron="lif", tau=2.0,
+                                   soft_reset=soft, v_threshold=0.5, v_reset=v_reset)
+    got = spk.cpu().float().view(T, B, N, H, d).permute(0, 1, 3, 2, 4)
+    assert torch.equal(got, a_ref)
+    assert 0 < int(got.sum()) < got.numel()
+
+
 def test_reference_api_linear_order_matches_core():
     """spike_ktv_popcount + spike_av_lif (reference linear order) == MFMA core."""
     T, B, H, N, d = 4, 2, 4, 70 - 6, 16

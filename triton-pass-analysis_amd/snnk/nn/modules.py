@@ -325,13 +325,16 @@ class FusedConvBNLIFPool(nn.Module):
         self.soft_reset, self.v_threshold, self.v_reset = soft_reset, float(v_threshold), v_reset
 
     def _dense(self, H, W):
-        """Dense-matrix form of the conv for a map of at most 2x2 (built once
-        per map size, on the weights' device)."""
-        key = (H, W)
+        """Dense-matrix form of the conv for a map of at most 2x2, built on the
+        weights' device and rebuilt whenever ``weight`` or ``bias`` is replaced
+        or changed in place (``load_state_dict``, ``.to()``, ``copy_``)."""
+        stamp = tuple((t.device, t.data_ptr(), t._version) for t in (self.weight, self.bias))
         cache = self.__dict__.setdefault("_dense_cache", {})
-        if key not in cache:
-            cache[key] = conv3x3_dense_weight(self.weight, self.bias, H, W, self.pool == "max")
-        return cache[key]
+        hit = cache.get((H, W))
+        if hit is None or hit[0] != stamp:
+            hit = (stamp, conv3x3_dense_weight(self.weight, self.bias, H, W, self.pool == "max"))
+            cache[(H, W)] = hit
+        return hit[1]
 
     def forward_nhwc(self, x_nhwc, out=None, tile_hint=-1):
         T, B, H, W, C = x_nhwc.shape
