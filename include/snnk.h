@@ -11,7 +11,9 @@
  *   - never allocates: every buffer is owned by the caller and passed as a
  *     raw device pointer;
  *   - sizes are int64_t; tensors are dense row-major in the layout stated;
- *   - is re-entrant and thread-safe (no mutable global state).
+ *   - is re-entrant and thread-safe (no mutable global state), except
+ *     snnk_conv3x3_bn_lif_noalloc, whose calls share one fixed scratch
+ *     region per GPU (see there).
  *
  * The reference operator each entry point replaces is cited as
  * path:line inside Xarlley/Triton-Pass-Analysis.
@@ -31,6 +33,7 @@ extern "C" {
 #define SNNK_EUNSUPPORTED -2   /* valid request this build does not cover   */
 #define SNNK_EALIGN       -3   /* pointer alignment the kernel requires      */
 #define SNNK_EWORKSPACE   -4   /* workspace missing or smaller than needed   */
+#define SNNK_ESCRATCH     -5   /* needs more than the fixed no-alloc scratch  */
 
 /* ---- element types --------------------------------------------------- */
 #define SNNK_F32   0
@@ -215,6 +218,27 @@ int snnk_conv3x3_bn_lif_ws(const uint16_t* x, const uint16_t* w, const float* bi
 int64_t snnk_conv3x3_bn_lif_ws_size(int64_t T, int64_t B, int64_t H, int64_t W,
                                     int64_t Cin, int64_t Cout, int32_t pool, int32_t preact,
                                     int32_t tile_hint, int32_t splits);
+/*
+ * snnk_conv3x3_bn_lif_ws without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ *
+ * Same arguments, tiling and results as snnk_conv3x3_bn_lif_ws; the split-K
+ * tickets and partial sums go to a fixed 32 MiB region of device memory inside
+ * the library (one per GPU, held until the process ends).  The call allocates
+ * nothing.  A plan that needs more than the region holds returns
+ * SNNK_ESCRATCH (splits = 1 needs none).  Every call on one GPU shares that
+ * GPU's region: calls that overlap on one GPU (two streams, two threads)
+ * race.  The first call on a GPU also enqueues a fill kernel that zeroes the
+ * region's ticket counters; every call leaves them at zero.
+ */
+int snnk_conv3x3_bn_lif_noalloc(const uint16_t* x, const uint16_t* w, const float* bias,
+                                uint16_t* spikes_out, float* preact_out,
+                                int64_t T, int64_t B, int64_t H, int64_t W,
+                                int64_t Cin, int64_t Cout, int32_t pool,
+                                float decay, float in_scale, float v_threshold,
+                                float v_reset, int32_t soft_reset, int32_t tile_hint,
+                                int32_t splits, void* stream);
 int snnk_linear_bias_lif_ws(const uint16_t* x, const uint16_t* w, const float* bias,
                             uint16_t* spikes_out, float* preact_out, int64_t T,
                             int64_t R, int64_t K, int64_t N, float decay,

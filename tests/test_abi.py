@@ -96,3 +96,20 @@ def test_workspace_pool_keys_by_device_and_stream():
         pool.get(0, 0x3000, 100, capturing=True)          # new stream inside a capture
     assert pool.get(0, 0x2000, 100, capturing=True) is b  # existing buffer is fine
 
+
+def test_noalloc_entry_point_rejects_oversized_plans_without_gpu():
+    """snnk_conv3x3_bn_lif_noalloc refuses a plan whose split-K partials exceed
+    its fixed 32 MiB region before any HIP call (fake, aligned pointers)."""
+    from snnk import _abi
+    lib = _abi.lib()
+    shape = (4, 32, 16, 16, 512, 512)
+    assert lib.snnk_conv3x3_bn_lif_ws_size(*shape, 0, 0, 2, 8) > (32 << 20)
+    fake = ctypes.c_void_p(1 << 20)
+    st = lib.snnk_conv3x3_bn_lif_noalloc(fake, fake, None, fake, None, *shape, 0,
+                                         0.5, 0.5, 1.0, 0.0, 0, 2, 8, None)
+    assert st == _abi.ESCRATCH
+    assert b"no-alloc" in lib.snnk_status_string(st)
+    # argument validation comes first, as in every entry point
+    st = lib.snnk_conv3x3_bn_lif_noalloc(fake, fake, None, fake, None, 4, 32, 16, 16, 500, 512,
+                                         0, 0.5, 0.5, 1.0, 0.0, 0, -1, 0, None)
+    assert st == _abi.EUNSUPPORTED

@@ -33,6 +33,7 @@
 // lane's source offsets are rebuilt only when the stage's tap changes.
 #include <algorithm>
 #include <cstddef>
+#include <mutex>
 #include <type_traits>
 
 #include "snnk_common.h"
@@ -999,6 +1000,77 @@ extern "C" int snnk_conv3x3_bn_lif_ws(const uint16_t* x, const uint16_t* w, cons
   if (st != SNNK_OK) return st;
   return run<9>(a, pool != 0, tile_hint, splits, true, workspace, workspace_bytes,
                 static_cast<hipStream_t>(stream));
+}
+
+// ---- no-allocation variant: a fixed scratch region in device memory ---------
+// The split-K tickets and partial sums of snnk_conv3x3_bn_lif_noalloc live in
+// this array instead of a caller workspace.  Each GPU the library runs on
+// holds its own copy for the life of the process.  In host code the name is
+// only a stand-in: the per-device address comes from hipGetSymbolAddress.
+constexpr int64_t kScratchBytes = int64_t{32} << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+
+__global__ void zero_words_kernel(unsigned int* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Device address of `scratch` on the current device, resolved on the first
+// call for that device; that call also clears the ticket region with a fill
+// kernel on `s` (ordered before the caller's conv on the same stream).
+int scratch_address(hipStream_t s, void** out) {
+  static std::mutex mu;
+  static void* addr[kMaxScratchDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return SNNK_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (p == nullptr || !aligned(p, 256)) return SNNK_EALIGN;
+    constexpr int kWords = static_cast<int>(kTicketBytes / 4);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((kWords + 255) / 256), dim3(256), 0, s,
+                       static_cast<unsigned int*>(p), kWords);
+    const int st = launch_status();
+    if (st != SNNK_OK) return st;
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return SNNK_OK;
+}
+
+}  // namespace
+
+extern "C" int snnk_conv3x3_bn_lif_noalloc(const uint16_t* x, const uint16_t* w,
+                                           const float* bias, uint16_t* spikes_out,
+                                           float* preact_out, int64_t T, int64_t B, int64_t H,
+                                           int64_t W, int64_t Cin, int64_t Cout, int32_t pool,
+                                           float decay, float in_scale, float v_threshold,
+                                           float v_reset, int32_t soft_reset, int32_t tile_hint,
+                                           int32_t splits, void* stream) {
+  ConvArgs a;
+  if (T == 0 || B == 0 || H == 0 || W == 0) return (T < 0 || B < 0 || H < 0 || W < 0) ? SNNK_EINVAL : SNNK_OK;
+  int st = conv_args(x, w, bias, spikes_out, preact_out, T, B, H, W, Cin, Cout, pool, decay,
+                     in_scale, v_threshold, v_reset, soft_reset, true, &a);
+  if (st != SNNK_OK) return st;
+  Plan p;
+  st = make_plan(a, tile_hint, splits, true, &p);
+  if (st != SNNK_OK) return st;
+  if (p.ws_bytes > kScratchBytes) return SNNK_ESCRATCH;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if (p.ws_bytes > 0) {
+    st = scratch_address(s, &ws);
+    if (st != SNNK_OK) return st;
+  }
+  return run<9>(a, pool != 0, tile_hint, splits, true, ws, kScratchBytes, s);
 }
 
 extern "C" int64_t snnk_conv3x3_bn_lif_ws_size(int64_t T, int64_t B, int64_t H, int64_t W,

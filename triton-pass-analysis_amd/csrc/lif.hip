@@ -269,6 +269,7 @@ extern "C" const char* snnk_status_string(int status) {
     case SNNK_EUNSUPPORTED: return "unsupported configuration";
     case SNNK_EALIGN: return "misaligned pointer";
     case SNNK_EWORKSPACE: return "workspace missing or too small";
+    case SNNK_ESCRATCH: return "needs more than the 32 MiB no-alloc scratch region (use the _ws entry point)";
     default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown status";
   }
 }

@@ -17,7 +17,7 @@ import torch
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libsnnk.so"
 
 # status codes (include/snnk.h)
-OK, EINVAL, EUNSUPPORTED, EALIGN, EWORKSPACE = 0, -1, -2, -3, -4
+OK, EINVAL, EUNSUPPORTED, EALIGN, EWORKSPACE, ESCRATCH = 0, -1, -2, -3, -4, -5
 # element types
 F32, BF16, F16, U8, I32 = 0, 1, 2, 3, 4
 # spike formats
@@ -84,6 +84,15 @@ PROTOTYPES: dict[str, list] = {
         _f32, _i32, _i32,      # v_reset, soft_reset, tile_hint
         _i32, _p, _i64,        # splits, workspace, workspace_bytes
         _p,                    # stream
+    ],
+    "snnk_conv3x3_bn_lif_noalloc": [
+        _p, _p, _p,            # x, w, bias
+        _p, _p,                # spikes_out, preact_out
+        _i64, _i64, _i64, _i64,  # T, B, H, W
+        _i64, _i64, _i32,      # Cin, Cout, pool
+        _f32, _f32, _f32,      # decay, in_scale, v_threshold
+        _f32, _i32, _i32,      # v_reset, soft_reset, tile_hint
+        _i32, _p,              # splits, stream
     ],
     "snnk_linear_bias_lif_ws": [
         _p, _p, _p,            # x, w, bias
