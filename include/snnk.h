@@ -298,9 +298,12 @@ int snnk_linear_mean_t(const uint16_t* x, const uint16_t* w, const float* bias, 
  *
  * q, k, v: bf16 spikes; element (t, token row r = b*N + n, head h, dim dd) at
  *   ptr + t*step + r*row + h*d + dd (q/k/v may be column slices of one
- *   [T][B*N][3*H*d] projection output).  N <= 64 tokens, d <= 64,
- *   d % 8 == 0; pointers 16-byte aligned, row and step strides multiples of 8,
- *   row strides below 2^23 elements (SNNK_EUNSUPPORTED otherwise).
+ *   [T][B*N][3*H*d] projection output).  d % 8 == 0, d <= 128; pointers
+ *   16-byte aligned, row and step strides multiples of 8, row strides below
+ *   2^23 elements (SNNK_EUNSUPPORTED otherwise).  Up to 64 tokens and 64
+ *   dims the counts are formed in the order (Q K^T) V on int8 MFMA; beyond,
+ *   in the order Q (K^T V) on bf16 MFMA (equal over the integers; d*N < 2^24),
+ *   where S is not formed: s_counts must then be NULL.
  * spikes_out: bf16, element (t, r, h*d + dd) at out + t*out_step + r*out_row + h*d + dd.
  * s_counts: NULL or int32 [T][B][H][N][N] (Q K^T); o_counts: NULL or int32
  *   [T][B][H][N][d] ((Q K^T) V).
@@ -313,6 +316,28 @@ int snnk_spike_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v
                          int64_t T, int64_t B, int64_t H, int64_t N, int64_t d,
                          float decay, float in_scale, float v_threshold,
                          float v_reset, int32_t soft_reset, void* stream);
+
+/*
+ * Fused (q @ kv) * scale -> multi-step LIF, the reference's linear attention
+ * order: per batch*head and step t, a = q_t kv_t, v = decay*v + in_scale*a,
+ * spike v >= v_threshold, hard reset to v_reset or soft reset.  The membrane
+ * stays in registers across T; a is never written.
+ *
+ * Replaces spike_av_lif / _spike_av_lif_kernel
+ *   snn_compiler/kernels/attention.py:49-137.
+ *
+ * q   [T][BH][N][d] of q_dtype (F32 / BF16 / F16), spikes 0/1
+ * kv  [T][BH][d][d] of kv_dtype (F32 or I32), e.g. K^T V counts
+ * spikes_out [T][BH][N][d] of q_dtype
+ * d <= 128.  q @ kv runs on bf16 MFMA with fp32 accumulation and kv as three
+ * bf16 parts whose sum is exactly its fp32 value: every product is exact, so
+ * integer kv (sums below 2^24) gives the exact count; real kv gives an fp32
+ * sum.  q values other than 0/1 are rounded to bf16.
+ */
+int snnk_spike_av_lif(const void* q, int32_t q_dtype, const void* kv, int32_t kv_dtype,
+                      void* spikes_out, int64_t T, int64_t BH, int64_t N, int64_t d,
+                      float decay, float in_scale, float v_threshold, float v_reset,
+                      int32_t soft_reset, void* stream);
 
 /*
  * Input layer: a static image presented at all T steps.  conv3x3 (pad 1)

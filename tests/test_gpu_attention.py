@@ -313,3 +313,99 @@ def test_fuse_spiking_attention_pass():
     assert all(isinstance(m, FusedSpikeAttention) for m in model)
     for m, y in zip(model, want):
         assert torch.equal(m(x), y)
+
+
+# ---- fused linear order: spike_av_lif and the large-shape core ----------------
+def _kv_counts(k, v):
+    return k.double().transpose(-1, -2) @ v.double()
+
+
+def _mid_threshold(a, in_scale):
+    """A threshold near the mean first-step input (a mix of spikes at any N)."""
+    return float(torch.tensor(float((a[0] * in_scale).mean()) + 1e-3, dtype=torch.float32))
+
+
+@pytest.mark.parametrize("T,B,H,N,d", [(4, 16, 8, 196, 96), (4, 2, 4, 70, 16), (3, 2, 3, 50, 40),
+                                       (2, 1, 2, 33, 20), (5, 2, 1, 256, 128), (1, 3, 2, 7, 8)])
+def test_spike_av_lif_fused_matches_oracle(T, B, H, N, d):
+    """(q @ kv) * scale -> LIF in one kernel (snn_compiler/kernels/attention.py:49-137),
+    bit-exact against the oracle on integer K^T V, for every q dtype and for
+    kv given as fp32 or int32."""
+    q = _spikes((T, B, H, N, d), 0.2, 400 + N)
+    k = _spikes((T, B, H, N, d), 0.2, 401 + N)
+    v = _spikes((T, B, H, N, d), 0.25, 402 + N)
+    kv = _kv_counts(k, v)
+    vth = _mid_threshold(q.double() @ kv, 0.0625)
+    ref = oa.spike_av_lif(q, kv.float(), scale=0.125, tau=2.0, v_threshold=vth)
+    assert 0 < int(ref.sum()) < ref.numel()
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        for kv_dt in (torch.float32, torch.int32):
+            s = spike_av_lif(q.to(DEV, dt), kv.to(DEV, kv_dt), scale=0.125, tau=2.0,
+                             v_threshold=vth)
+            assert s.dtype == dt and s.shape == q.shape
+            assert torch.equal(s.cpu().float(), ref), (dt, kv_dt)
+
+
+@pytest.mark.parametrize("soft,v_reset,decay_input", [(True, 0.0, True), (False, 0.25, True),
+                                                       (False, 0.0, False)])
+def test_spike_av_lif_reset_modes(soft, v_reset, decay_input):
+    T, B, H, N, d = 4, 2, 3, 45, 24
+    q = _spikes((T, B, H, N, d), 0.3, 11)
+    kv = _kv_counts(_spikes((T, B, H, N, d), 0.3, 12), _spikes((T, B, H, N, d), 0.3, 13))
+    a = q.double() @ kv
+    sc = 0.125 if decay_input else 0.0625
+    ref, _, _ = on.lif_multistep((a * sc).float(), neuron="lif", tau=2.0, decay_input=decay_input,
+                                 soft_reset=soft, v_threshold=0.5, v_reset=v_reset)
+    s = spike_av_lif(q.to(DEV), kv.float().to(DEV), scale=sc, tau=2.0, decay_input=decay_input,
+                     v_threshold=0.5, v_reset=v_reset, soft_reset=soft)
+    assert torch.equal(s.cpu(), ref)
+
+
+def test_spike_av_lif_real_valued_kv():
+    """kv with fractional values: the three bf16 parts make every product exact,
+    so the kernel's pre-activation is an fp32 sum of exact terms; spikes agree
+    with a float64 reference except within rounding distance of threshold."""
+    T, B, H, N, d = 4, 2, 2, 64, 48
+    g = torch.Generator().manual_seed(21)
+    q = _spikes((T, B, H, N, d), 0.3, 22)
+    kv = torch.randn(T, B, H, d, d, generator=g) * 3.0
+    a = q.double() @ kv.double()
+    v = torch.zeros(a.shape[1:], dtype=torch.float64)
+    ref, near = [], []
+    for t in range(T):
+        h = 0.5 * v + 0.0625 * a[t]
+        ref.append((h >= 0.5).float())
+        near.append((h - 0.5).abs() < 1e-4)
+        v = torch.where(h >= 0.5, torch.zeros_like(h), h)
+    ref, near = torch.stack(ref), torch.stack(near)
+    s = spike_av_lif(q.to(DEV), kv.to(DEV), scale=0.125, tau=2.0, v_threshold=0.5).cpu()
+    bad = (s != ref)
+    assert float(bad.float().mean()) <= 1e-3
+    # a flip at t can only come from a near-threshold value at some step <= t
+    assert bool((~bad[0] | near[0]).all())
+
+
+@pytest.mark.parametrize("T,B,H,N,d", [(4, 16, 8, 196, 96), (4, 2, 2, 100, 64), (2, 3, 1, 65, 8),
+                                       (3, 2, 2, 64, 72), (2, 1, 2, 300, 128), (3, 2, 2, 20, 104)])
+def test_attention_core_large_shapes_exact(T, B, H, N, d):
+    """Past 64 tokens / 64 dims the core runs Q (K^T V): O counts, S counts (binary
+    GEMM) and spikes bit-exact against integer products and the oracle LIF."""
+    D = H * d
+    qkv = _spikes((T, B * N, 3 * D), 0.2, 7000 + N + d)
+    qd = qkv.to(DEV, torch.bfloat16)
+    q, k, v = qd[..., :D], qd[..., D:2 * D], qd[..., 2 * D:]
+    hq = lambda s: s.view(T, B, N, H, d).permute(0, 1, 3, 2, 4).long()  # noqa: E731
+    qh, kh, vh = hq(qkv[..., :D]), hq(qkv[..., D:2 * D]), hq(qkv[..., 2 * D:])
+    S_ref = qh @ kh.transpose(-1, -2)
+    O_ref = qh @ (kh.transpose(-1, -2) @ vh)
+    vth = _mid_threshold(O_ref.double(), 0.0625)
+    spk, S, O = spike_attention(q, k, v, B=B, N=N, heads=H, scale=0.125, tau=2.0,
+                                v_threshold=vth, return_counts=True)
+    assert torch.equal(O_ref, S_ref @ vh)
+    assert torch.equal(O.cpu().long(), O_ref)
+    assert torch.equal(S.cpu().long(), S_ref)
+    a_ref = oa.spike_av_lif(qh.float(), (kh.transpose(-1, -2) @ vh).float(), scale=0.125,
+                            tau=2.0, v_threshold=vth)
+    got = spk.cpu().float().view(T, B, N, H, d).permute(0, 1, 3, 2, 4)
+    assert torch.equal(got, a_ref)
+    assert 0 < int(got.sum()) < got.numel()

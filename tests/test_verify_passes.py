@@ -13,7 +13,7 @@ import torch.nn as nn
 
 from snnk.verify import compare_models, assert_equivalent
 from snnk.passes import fuse_snn_model, fuse_modules_path, fuse_conv_bn_add_neuron_path
-from snnk.passes.fuse import _neuron_kwargs
+from snnk.passes.fuse import NeuronSpec
 from snnk.nn import (
     LIFNode, IFNode, FusedConvBNNeuron, FusedConvNeuron, FusedLinearNeuron, FusedConvBNLIFPool,
     FusedConvBNAddNeuron,
@@ -157,17 +157,37 @@ class _SJLif(nn.Module):
 _SJLif.__name__ = "LIFNode"
 
 
-def test_neuron_kwargs_duck_typing():
-    kw = _neuron_kwargs(_SJLif())
-    assert kw == dict(neuron="lif", tau=4.0, decay_input=False, soft_reset=True,
-                      v_threshold=0.7, v_reset=0.0, layout="NCHW")
-    kw = _neuron_kwargs(IFNode(v_threshold=0.5, soft_reset=True))
+def test_neuron_spec_duck_typing():
+    spec = NeuronSpec.of(_SJLif())
+    assert spec.kwargs("NCHW") == dict(neuron="lif", decay=None, tau=4.0, decay_input=False,
+                                       soft_reset=True, v_threshold=0.7, v_reset=0.0,
+                                       layout="NCHW")
+    kw = NeuronSpec.of(IFNode(v_threshold=0.5, soft_reset=True)).kwargs()
     assert kw["neuron"] == "if" and kw["soft_reset"] and kw["v_threshold"] == 0.5
+    assert "tau" not in kw and "layout" not in kw
+    assert NeuronSpec.kind_of(nn.ReLU()) is None
+    with pytest.raises(TypeError):
+        NeuronSpec.of(nn.ReLU())
     seq = nn.Sequential(nn.Conv2d(8, 8, 3, padding=1), nn.BatchNorm2d(8).eval(), _SJLif(),
                         nn.Flatten(), nn.Linear(8, 4), LIFNode(tau=3.0))
     m, n = fuse_snn_model(seq.eval())
     assert n == 2 and isinstance(m[0], FusedConvBNNeuron) and isinstance(m[2], FusedLinearNeuron)
     assert m[0].soft_reset and m[0].tau == 4.0 and m[2].tau == 3.0
+
+
+def test_fuse_snn_model_recurses_into_non_sequential_containers():
+    class Net(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.stem = nn.Sequential(nn.Conv2d(3, 8, 3, padding=1), IFNode())
+            self.blocks = nn.ModuleList([nn.Sequential(nn.Linear(8, 8), LIFNode()),
+                                         nn.Sequential(nn.ReLU())])
+    net = Net().eval()
+    m, n = fuse_snn_model(net)
+    assert m is net and n == 2
+    assert isinstance(net.stem[0], FusedConvNeuron) and len(net.stem) == 1
+    assert isinstance(net.blocks[0][0], FusedLinearNeuron)
+    assert isinstance(net.blocks[1][0], nn.ReLU)
 
 
 def test_fuse_modules_path_and_residual():
@@ -190,3 +210,5 @@ def test_fuse_modules_path_and_residual():
     assert isinstance(b.conv2, nn.Identity) and isinstance(b.bn2, nn.Identity)
     with pytest.raises(ValueError):
         fuse_modules_path(b, [("a", "b")])
+    with pytest.raises(TypeError):
+        fuse_modules_path(b, [("fc", "bn1", "neuron1")])     # Linear is no Conv2d

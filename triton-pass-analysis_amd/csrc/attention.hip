@@ -18,6 +18,16 @@
 #include "snnk_common.h"
 
 namespace snnk {
+
+// Linear-order path for more than 64 tokens or dims (attention_linear.hip).
+int spike_attention_linear(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                           int64_t q_row, int64_t k_row, int64_t v_row, int64_t q_step,
+                           int64_t k_step, int64_t v_step, uint16_t* spikes_out,
+                           int64_t out_row, int64_t out_step, int32_t* o_counts, int64_t T,
+                           int64_t B, int64_t H, int64_t N, int64_t d, float decay,
+                           float in_scale, float v_threshold, float v_reset, int32_t soft_reset,
+                           hipStream_t s);
+
 namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -295,7 +305,10 @@ extern "C" int snnk_spike_attention(const uint16_t* q, const uint16_t* k, const 
   if (T < 0 || B < 0 || H <= 0 || N < 0 || d <= 0) return SNNK_EINVAL;
   if (T == 0 || B == 0 || N == 0) return SNNK_OK;
   if (q == nullptr || k == nullptr || v == nullptr || spikes_out == nullptr) return SNNK_EINVAL;
-  if (N > kMaxTok || d > kMaxDim || d % 8 != 0) return SNNK_EUNSUPPORTED;
+  if (d % 8 != 0) return SNNK_EUNSUPPORTED;
+  // more than 64 tokens or dims: the linear order Q (K^T V), which has no S
+  const bool linear = N > kMaxTok || d > kMaxDim;
+  if (linear && s_counts != nullptr) return SNNK_EUNSUPPORTED;
   // 16-byte chunk loads: every row start and head offset on a 16-byte boundary
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || q_row % 8 || k_row % 8 ||
       v_row % 8 || q_step % 8 || k_step % 8 || v_step % 8)
@@ -304,6 +317,11 @@ extern "C" int snnk_spike_attention(const uint16_t* q, const uint16_t* k, const 
   if (B * H > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
   // byte offsets of a step's token rows stay below 2^31 (buffer offsets)
   if (std::max(q_row, std::max(k_row, v_row)) >= (int64_t{1} << 23)) return SNNK_EUNSUPPORTED;
+  if (linear)
+    return spike_attention_linear(q, k, v, q_row, k_row, v_row, q_step, k_step, v_step,
+                                  spikes_out, out_row, out_step, o_counts, T, B, H, N, d, decay,
+                                  in_scale, v_threshold, v_reset, soft_reset,
+                                  static_cast<hipStream_t>(stream));
   AttnArgs a{};
   a.q = q; a.k = k; a.v = v;
   a.q_row = q_row; a.k_row = k_row; a.v_row = v_row;

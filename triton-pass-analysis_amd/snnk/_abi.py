@@ -128,6 +128,13 @@ PROTOTYPES: dict[str, list] = {
         _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
         _i32, _p,              # soft_reset, stream
     ],
+    "snnk_spike_av_lif": [
+        _p, _i32, _p, _i32,    # q, q_dtype, kv, kv_dtype
+        _p,                    # spikes_out
+        _i64, _i64, _i64, _i64,  # T, BH, N, d
+        _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
+        _i32, _p,              # soft_reset, stream
+    ],
     "snnk_conv3x3_image_lif": [
         _p, _p, _p, _p,        # image, w, bias, spikes_out
         _i64, _i64, _i64,      # T, B, Cin

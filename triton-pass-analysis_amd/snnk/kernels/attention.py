@@ -3,10 +3,14 @@
 * ``spike_ktv_popcount``: bit-exact K^T V through bit packing along the
   token axis and a popcount GEMM (reference attention.py:245-258).
 * ``spike_av_lif``: the reference's fused ``(q @ kv) * scale -> LIF``
-  (attention.py:107-137): integer q @ kv on the GPU, then the HIP LIF kernel.
-* ``spike_attention``: the attention core on int8 MFMA straight from Q, K, V
-  spikes -- integer Q K^T and (Q K^T) V, then the LIF -- with the counts
-  optionally returned (csrc/attention.hip).
+  (attention.py:107-137) in one HIP kernel (csrc/attention_linear.hip): the
+  product runs on bf16 MFMA with kv split into exact bf16 parts, the
+  membrane stays in registers across T and ``q @ kv`` is never stored.
+* ``spike_attention``: the attention core straight from Q, K, V spikes: the
+  quadratic order (Q K^T) V on int8 MFMA up to 64 tokens and 64 dims per
+  head (csrc/attention.hip), the linear order Q (K^T V) on bf16 MFMA beyond
+  (csrc/attention_linear.hip; equal counts over the integers), then the LIF,
+  with the integer counts optionally returned.
 * ``spike_self_attention``: the whole SSA block on tokens [T, B, N, D]:
   fused QKV Linear + BN + LIF, the attention core, and the output Linear + BN.
 """
@@ -46,6 +50,23 @@ def spike_ktv_popcount(k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
     return out.reshape(T, B, H, D, D)
 
 
+def spike_ktv(k: torch.Tensor, v: torch.Tensor, *, algo: str = "auto") -> torch.Tensor:
+    """K^T V for spikes ``[T, B, heads, N, d]`` -> fp32 ``[T, B, heads, d, d]``.
+
+    Reference: snn_compiler/kernels/attention.py:177-187 (an fp32 dot product
+    over the tokens).  Here an exact binary GEMM of the spikes packed along
+    the token axis (nonzero counts as 1): the MFMA kernels where the shape
+    allows, the VALU popcount kernel otherwise.
+    """
+    T, B, H, N, D = k.shape
+    assert v.shape == k.shape, f"k {tuple(k.shape)} and v {tuple(v.shape)} must match"
+    TBH = T * B * H
+    kp = _pack_N(k.reshape(TBH, N, D))
+    vp = _pack_N(v.reshape(TBH, N, D))
+    out = _gemm_packed(kp, vp, N, signed=False, algo=algo, out_dtype=torch.float32)
+    return out.reshape(T, B, H, D, D)
+
+
 def _lif_scale(tau, decay, decay_input, scale):
     dec = (1.0 if tau is None else 1.0 - 1.0 / tau) if decay is None else float(decay)
     base = (1.0 / tau) if (decay_input and tau is not None) else 1.0
@@ -55,32 +76,62 @@ def _lif_scale(tau, decay, decay_input, scale):
 def spike_av_lif(q, kv, *, scale, tau=2.0, decay=None, decay_input=True, v_threshold=0.5,
                  v_reset=0.0, soft_reset=False):
     """``(q @ kv) * scale -> LIF`` with q [T,B,heads,N,d] spikes and kv
-    [T,B,heads,d,d] integer counts; returns spikes like q.
+    [T,B,heads,d,d] counts; returns spikes like q (same dtype).
 
     Reference: snn_compiler/kernels/attention.py:107-137 (the scale is folded
-    into the LIF input scale, as there).  q @ kv is an exact integer product
-    (fp32 GEMM of small integers), the neuron runs in the HIP LIF kernel.
+    into the LIF input scale, as there).  One HIP kernel: q @ kv on bf16 MFMA
+    with kv as three bf16 parts whose sum is exact, fp32 accumulation (exact
+    for integer kv), the LIF in registers across T.  q must hold spikes
+    (0/1); kv may be fp32 or int32 (other dtypes are converted to fp32).
     """
-    assert q.is_cuda and kv.is_cuda
+    assert q.is_cuda and kv.is_cuda and q.device == kv.device
+    assert q.ndim == 5 and kv.ndim == 5, "q [T,B,H,N,d] and kv [T,B,H,d,d]"
     T, B, H, N, D = q.shape
-    a = torch.matmul(q.float().contiguous(), kv.float().contiguous()).reshape(T, -1)
+    assert tuple(kv.shape) == (T, B, H, D, D), \
+        f"kv {tuple(kv.shape)} must be [T,B,H,d,d] = {(T, B, H, D, D)}"
+    assert q.dtype in (torch.float32, torch.bfloat16, torch.float16), q.dtype
+    if kv.dtype not in (torch.float32, torch.int32):
+        kv = kv.float()
+    qc, kvc = q.contiguous(), kv.contiguous()
     dec, in_scale = _lif_scale(tau, decay, decay_input, scale)
-    s = torch.empty_like(a)
-    launch_lif(a, thr=(THR_SCALAR, None, float(v_threshold)), spikes=s, decay=dec,
-               in_scale=in_scale, v_reset=v_reset, soft_reset=soft_reset)
-    return s.reshape(T, B, H, N, D).to(q.dtype)
+    out = torch.empty_like(qc)
+    if out.numel() == 0:
+        return out
+    with torch.cuda.device(q.device):
+        _abi.call("snnk_spike_av_lif", qc.data_ptr(), _abi.dtype_code(qc.dtype), kvc.data_ptr(),
+                  _abi.dtype_code(kvc.dtype), out.data_ptr(), T, B * H, N, D, float(dec),
+                  float(in_scale), float(v_threshold), float(v_reset), 1 if soft_reset else 0,
+                  _abi.stream(q.device))
+    return out
+
+
+def _s_counts(q, k, *, B: int, N: int, heads: int) -> torch.Tensor:
+    """Integer Q K^T [T, B, heads, N, N] from spike column slices [T, B*N, heads*d],
+    through the bit-packed binary GEMM (the linear-order core forms no S)."""
+    T = q.shape[0]
+    d = q.shape[2] // heads
+
+    def heads_major(s):  # [T, B*N, H*d] -> [T, B, H, N, d]
+        return s.reshape(T, B, N, heads, d).permute(0, 1, 3, 2, 4)
+
+    qp = pack_bits(heads_major(q), dim=-1)   # [T, B, H, N, words]
+    kp = pack_bits(heads_major(k), dim=-1)
+    return _gemm_packed(qp, kp, d, signed=False, algo="auto", out_dtype=torch.int32)
 
 
 def spike_attention(q, k, v, *, B: int, N: int, heads: int, scale: float, tau: float = 2.0,
                     decay: float | None = None, decay_input: bool = True,
                     v_threshold: float = 0.5, v_reset: float = 0.0, soft_reset: bool = False,
                     out: torch.Tensor | None = None, return_counts: bool = False):
-    """Attention core on int8 MFMA.
+    """Attention core: the LIF of ``scale * (Q K^T) V`` per (batch, head).
 
     q, k, v: bf16 spikes ``[T, B*N, heads*d]`` (any row stride, e.g. column
-    slices of one QKV projection output).  Returns spikes ``[T, B*N, heads*d]``
-    bf16, and with ``return_counts`` also int32 ``S = Q K^T`` [T,B,heads,N,N]
-    and ``O = (Q K^T) V`` [T,B,heads,N,d].
+    slices of one QKV projection output); d % 8 == 0 and d <= 128.  Returns
+    spikes ``[T, B*N, heads*d]`` bf16, and with ``return_counts`` also int32
+    ``S = Q K^T`` [T,B,heads,N,N] and ``O = (Q K^T) V`` [T,B,heads,N,d].
+    Up to 64 tokens and 64 dims the core runs in the quadratic order on int8
+    MFMA; beyond, in the linear order Q (K^T V) (equal integers), and S then
+    comes from the bit-packed binary GEMM.
     """
     for t in (q, k, v):
         assert t.is_cuda and t.dtype == torch.bfloat16 and t.ndim == 3 and t.stride(2) == 1
@@ -90,9 +141,11 @@ def spike_attention(q, k, v, *, B: int, N: int, heads: int, scale: float, tau: f
     dec, in_scale = _lif_scale(tau, decay, decay_input, scale)
     if out is None:
         out = torch.empty(T, R, HD, device=q.device, dtype=torch.bfloat16)
+    linear = N > 64 or d > 64
     S = O = None
     if return_counts:
-        S = torch.empty(T, B, heads, N, N, device=q.device, dtype=torch.int32)
+        if not linear:
+            S = torch.empty(T, B, heads, N, N, device=q.device, dtype=torch.int32)
         O = torch.empty(T, B, heads, N, d, device=q.device, dtype=torch.int32)
     with torch.cuda.device(q.device):
         _abi.call("snnk_spike_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(),
@@ -100,6 +153,8 @@ def spike_attention(q, k, v, *, B: int, N: int, heads: int, scale: float, tau: f
                   out.data_ptr(), out.stride(1), out.stride(0), _abi.ptr(S), _abi.ptr(O),
                   T, B, heads, N, d, float(dec), float(in_scale), float(v_threshold),
                   float(v_reset), 1 if soft_reset else 0, _abi.stream(q.device))
+        if return_counts and linear:
+            S = _s_counts(q, k, B=B, N=N, heads=heads)
     return (out, S, O) if return_counts else out
 
 
