@@ -248,6 +248,42 @@ int snnk_linear_bias_lif_ws(const uint16_t* x, const uint16_t* w, const float* b
 int64_t snnk_linear_bias_lif_ws_size(int64_t T, int64_t R, int64_t K, int64_t N,
                                      int32_t preact, int32_t tile_hint, int32_t splits);
 
+/* ---- activation formats of the _act entry points ---------------------- */
+#define SNNK_ACT_BF16 0   /* 0/1 as bf16, NHWC / [T][R][K]                       */
+#define SNNK_ACT_BITS 1   /* packed: bit c%32 of uint32 word c/32 of each pixel's
+                             (row's) channels, LSB first: [T][B][H][W][C/32]    */
+
+/*
+ * snnk_conv3x3_bn_lif_ws / snnk_linear_bias_lif_ws with a choice of
+ * activation formats: x (x_fmt) and the spikes (out_fmt) as bf16 0/1 or as
+ * packed bits (SNNK_ACT_BITS, 16x fewer bytes; the layout SNNK_SPIKE_BITS of
+ * snnk_lif_forward gives for channels-last maps).  Packed x is expanded to
+ * bf16 0/1 on its way into the MFMA operand stage; packed spikes are written
+ * one 32-channel word per pixel and step.  Same tiling, results and
+ * workspace contract as the _ws entry points (size it with *_ws_size, preact
+ * = 0); LIF only.  Packed words need 4-byte alignment, bf16 x 16 bytes.
+ *
+ * Replaces the same layer pairs as snnk_conv3x3_bn_lif / snnk_linear_bias_lif,
+ * with the bit-packed activation format of _pack_N
+ * (snn_compiler/kernels/attention.py:195-214) between layers, the
+ * "fused-LIF-pack" the reference lists as future work
+ * (Document/Skill/snn-compiler-spiking-attention.md:232).
+ */
+int snnk_conv3x3_bn_lif_act(const void* x, int32_t x_fmt, const uint16_t* w, const float* bias,
+                            void* spikes_out, int32_t out_fmt,
+                            int64_t T, int64_t B, int64_t H, int64_t W,
+                            int64_t Cin, int64_t Cout, int32_t pool,
+                            float decay, float in_scale, float v_threshold,
+                            float v_reset, int32_t soft_reset, int32_t tile_hint,
+                            int32_t splits, void* workspace, int64_t workspace_bytes,
+                            void* stream);
+int snnk_linear_bias_lif_act(const void* x, int32_t x_fmt, const uint16_t* w, const float* bias,
+                             void* spikes_out, int32_t out_fmt, int64_t T, int64_t R,
+                             int64_t K, int64_t N, float decay, float in_scale,
+                             float v_threshold, float v_reset, int32_t soft_reset,
+                             int32_t tile_hint, int32_t splits, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+
 /*
  * snnk_linear_bias_lif_ws followed by an OR over each group of four adjacent
  * output columns: spikes_out [T][R][N/4] bf16, column c = max of the spikes of

@@ -32,667 +32,12 @@
 // an NBUF-deep LDS ring filled by direct global->LDS buffer loads; each
 // lane's source offsets are rebuilt only when the stage's tap changes.
 #include <algorithm>
-#include <cstddef>
 #include <mutex>
-#include <type_traits>
 
-#include "snnk_common.h"
+#include "conv_kernel.h"
 
 namespace snnk {
 namespace {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-constexpr int kKS = 64;           // K per stage
-constexpr int kRow = kKS;         // LDS row pitch in bf16 (128 B, eight 16-byte chunks)
-constexpr int kRowBytes = kRow * 2;
-constexpr int kDmaRows = 1024 / kRowBytes;  // rows filled by one wave-wide 16-byte load
-constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
-// buffer-access cache policy sc0 | sc1: system-coherent, through to memory
-// past the XCD's L2 (the split-K partial sums of blocks on other XCDs)
-constexpr int kSystemCoherent = 17;
-// Offset base past every operand: kFar plus any stage delta (< 2^31) stays
-// below 2^32 and at or past the end of an operand of at most kFar bytes, so
-// such a load reads zeros (padding taps, rows past the end, steps past T,
-// columns past Cout, the half of a last stage past K).
-constexpr uint32_t kFar = 0x80000000u;
-
-// Wait until at most N of this wave's vector-memory loads are outstanding,
-// then meet the other waves of the block.  Written out so that no release
-// fence (and its full vmcnt(0) wait) is attached to the barrier.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-// Wait for a ring stage whose `later` successors (at most MAXL, kSEG loads
-// each) may still be in flight; a stage past the end issues no loads, so the
-// tail of the K loop waits for fewer.
-template <int kSEG, int MAXL>
-__device__ __forceinline__ void wait_stages_barrier(int later) {
-  static_assert(MAXL >= 0 && MAXL <= 3, "ring depth");
-  if (later >= MAXL) wait_vmcnt_barrier<kSEG * MAXL>();
-  else if (later == 2) wait_vmcnt_barrier<kSEG * 2>();
-  else if (later == 1) wait_vmcnt_barrier<kSEG>();
-  else wait_vmcnt_barrier<0>();
-}
-
-// 16-byte chunk c of LDS row r is stored at chunk c ^ key(r).  gfx950 serves
-// a ds_read_b128 16 lanes per pass over 64 four-byte banks; the fragment
-// reads (16 consecutive rows, one chunk column) then hit 16 distinct 16-byte
-// bank groups, and the key is also conflict-free for 8-lane passes.  It
-// depends on row bits 0-3 only, so 32-row fragment tiles share it.
-__device__ __forceinline__ int swz_key(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
-__device__ __forceinline__ int swz(int r, int c) { return c ^ swz_key(r); }
-
-// MODE_MEAN (Linear only): fp32 (x W^T + b) averaged over the T steps,
-// out [R][N], for a classifier head whose logits are read as their mean over T.
-enum { MODE_LIF = 0, MODE_PREACT = 1, MODE_MEAN = 2 };
-
-struct ConvArgs {
-  const uint16_t* x;
-  const uint16_t* w;
-  const float* bias;
-  uint16_t* out;
-  float* pre;
-  int T, B, H, W, Cin, Cout, Ho, Wo;
-  int n_quads;        // quads in one time step
-  int n_stages;       // K / 32
-  FastDiv div_cin;
-  FastDiv div_howo, div_wo, div_hw, div_w;  // row index -> (b, y, x)
-  uint32_t x_tstride_b;  // bytes of one input step (B*H*W*Cin*2)
-  uint32_t x_bytes;      // bytes of x (T steps), at most kFar
-  uint32_t w_bytes;      // bytes of w, at most kFar
-  int64_t o_tstride;     // B*Ho*Wo*Cout
-  int tiles_m, tiles_n;  // output tiles along rows (quads) and Cout
-  FastDiv div_tiles_m, div_tiles_n;
-  // cross-block split-K: `splits` blocks share one output tile, each over
-  // `stages_per_split` K stages; partial sums go to `partials`, the last
-  // block of a tile (ticket in `tickets`) reduces them in split order
-  int splits, stages_per_split;
-  float* partials;
-  unsigned int* tickets;
-  float decay, in_scale, vth, v_reset;
-  int soft_reset;
-};
-
-static_assert(offsetof(ConvArgs, x) / 64 == 0 && offsetof(ConvArgs, div_cin) / 64 == 1 &&
-                  offsetof(ConvArgs, o_tstride) / 64 == 2 && offsetof(ConvArgs, tickets) / 64 == 3 &&
-                  sizeof(ConvArgs) <= 256,
-              "the kernel touches one field per 64-byte line of ConvArgs");
-
-template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF>
-struct Cfg {
-  static constexpr int kWaves = WM * WN * KSPLIT;
-  static constexpr int kThreads = 64 * kWaves;
-  static constexpr int BM = WM * TM * 32;
-  static constexpr int BN = WN * TN * 32;
-  static constexpr int kQuads = BM / 16;                    // quads per block
-  // operand stages arrive by 16-byte direct-to-LDS loads, one wave-wide
-  // load filling kDmaRows rows (1 KB); the WM*WN waves of a K group share them
-  static constexpr int kSegA = BM / kDmaRows;
-  static constexpr int kSegB = BN / kDmaRows;
-  static constexpr int kGroupWaves = WM * WN;
-  static_assert(kSegA % kGroupWaves == 0 && kSegB % kGroupWaves == 0,
-                "segments must split evenly over a group's waves");
-  static constexpr int kAPer = kSegA / kGroupWaves;  // per wave: A segments first,
-  static constexpr int kBPer = kSegB / kGroupWaves;  // then B segments
-  static constexpr int kSegPer = kAPer + kBPer;
-  static constexpr int kStageBytes = KSPLIT * (BM + BN) * kRowBytes;
-  static constexpr int kBuf = NBUF;  // ring of operand stages in LDS
-  static constexpr int kLdsBytes = kBuf * kStageBytes;
-  static constexpr int kRedBytes = (KSPLIT - 1) * WM * WN * TM * TN * 16 * 64 * 4;
-  static constexpr int kSmem = kLdsBytes > kRedBytes ? kLdsBytes : kRedBytes;
-  static_assert(NBUF >= 2 && kSmem <= 160 * 1024, "LDS ring must fit 160 KB");
-};
-
-__device__ __forceinline__ uint16_t spike_bf16(bool s) { return s ? 0x3F80u : 0u; }
-
-// v of the lane CTRL names within each group of 4 lanes (DPP quad_perm)
-template <int CTRL>
-__device__ __forceinline__ uint32_t quad_dpp(uint32_t v) {
-  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
-}
-
-// TAPS = 9: 3x3 conv, pad 1.  TAPS = 1: 1x1 conv, i.e. a Linear layer over
-// the rows of [T][rows][Cin] (H = 1, W = rows).
-template <int TAPS>
-__device__ __forceinline__ int tap_dy(int tap) { return TAPS == 9 ? tap / 3 - 1 : 0; }
-template <int TAPS>
-__device__ __forceinline__ int tap_dx(int tap) { return TAPS == 9 ? tap % 3 - 1 : 0; }
-
-template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int MODE, int TAPS>
-__global__ __launch_bounds__(64 * WM * WN * KSPLIT)
-void conv3x3_kernel(ConvArgs a) {
-  using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF>;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::kSmem];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kg = wave / (WM * WN);
-  const int wmn = wave - kg * (WM * WN);
-  const int wm = wmn / WN, wn = wmn - wm * WN;
-  {
-    // One field of each 64-byte line of the arguments, loaded together at
-    // entry: on first use the scalar loads would go out one line at a time,
-    // each a cold miss (0.2 us off the time to the first operand stage).
-    const uint32_t l0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(a.x));
-    const uint32_t l1 = a.div_cin.m;
-    const uint32_t l2 = static_cast<uint32_t>(a.o_tstride);
-    const uint32_t l3 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(a.tickets));
-    asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3));
-  }
-  // Workgroups are dealt to the 8 XCDs round-robin by id; id -> tile is
-  // remapped so that each XCD runs one contiguous range of tiles.  Without
-  // split-K the range is row-tile major (an XCD's L2 holds its rows'
-  // activations); with split-K it is (split, Cout tile) major, so each XCD
-  // streams its own slice of the weights once.
-  const int n_mn = a.tiles_m * a.tiles_n;
-  const int n_tiles = n_mn * a.splits;
-  const int per_xcd = (n_tiles + 7) / 8;
-  const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if (tile >= n_tiles) return;  // whole workgroup: no barrier is left waiting
-  int tm, tn, split;
-  // (multiply-high dividers: a runtime integer division is ~30 instructions
-  // of straight-line code, fetched cold at the start of every launch)
-  if (a.splits == 1) {
-    tm = static_cast<int>(fdiv(static_cast<uint32_t>(tile), a.div_tiles_n));
-    tn = tile - tm * a.tiles_n;
-    split = 0;
-  } else {
-    const int rest = static_cast<int>(fdiv(static_cast<uint32_t>(tile), a.div_tiles_m));
-    tm = tile - rest * a.tiles_m;
-    split = static_cast<int>(fdiv(static_cast<uint32_t>(rest), a.div_tiles_n));
-    tn = rest - split * a.tiles_n;
-  }
-  const int mn = tm * a.tiles_n + tn;  // output tile id
-  const int quad0 = tm * C::kQuads;
-  const int n0 = tn * C::BN;
-  // this block's K stages [st_begin, st_end)
-  const int st_begin = split * a.stages_per_split;
-  const int st_end = min(a.n_stages, st_begin + a.stages_per_split);
-  const int HW = a.H * a.W;
-  constexpr int kPartFloats = TM * TN * 16 * 64;  // a wave's share of an output tile
-  const int K = TAPS * a.Cin;
-
-  // Operands are read through range-checked buffer descriptors: an offset
-  // at or past the end returns zeros, which is how padding taps, rows past
-  // the last pixel, steps past T and columns past Cout are filled.
-  const __amdgpu_buffer_rsrc_t xr =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), 0, a.x_bytes, kRsrcWord3);
-  const __amdgpu_buffer_rsrc_t wr =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.w), 0, a.w_bytes, kRsrcWord3);
-
-  // ---- segment geometry (fixed for the whole kernel) ----------------------
-  // A segment q of a group's stage is A rows kDmaRows*q.. (1 KB), B segment
-  // q is B rows kDmaRows*q..; wave wmn of the group loads A segments
-  // wmn + i*kGroupWaves (i < kAPer) and the same B segments (i < kBPer).
-  // Lane l writes row kDmaRows*q + l/8, chunk slot l%8, and so reads source
-  // chunk c = slot ^ key(row).  Chunks 0-3 hold k0..k0+31 of the stage, chunks
-  // 4-7 k0+32..k0+63: the lane's half is h = c/4, and since key(row) has bit
-  // 2 = (q ^ row) & 1, h = h0 ^ (q & 1) with h0 = (slot/4) ^ (l/8 & 1).  With
-  // Cin % 64 == 32 the two halves of a stage may fall in different taps.
-  const int lrow = lane >> 3, slot = lane & 7;
-  const uint32_t h0 = static_cast<uint32_t>((slot >> 2) ^ (lrow & 1));
-  uint32_t s_base[C::kSegPer];  // A: bytes of (t, b, y, x) + 16*(c%4); B: bytes of (n, c) or kFar
-  uint32_t s_ok[C::kAPer];      // A: bit tap set when the row exists and the tap's source
-                                // pixel is inside the image
-#pragma unroll
-  for (int i = 0; i < C::kSegPer; ++i) {
-    if (i < C::kAPer) {
-      const int q = wmn + i * C::kGroupWaves;
-      const int r = kDmaRows * q + lrow;
-      const int rr = r & 31;
-      const int pq = rr >> 3, gr = (rr >> 2) & 1, t = rr & 3;
-      const int quad = quad0 + (r >> 5) * 2 + gr;
-      int b = 0, y = 0, xx = 0;
-      const bool row_ok = quad < a.n_quads;
-      uint32_t ok = 0;
-      if (row_ok) {
-        if constexpr (POOL && TAPS == 9) {
-          b = static_cast<int>(fdiv(static_cast<uint32_t>(quad), a.div_howo));
-          const int r2 = quad - b * a.Ho * a.Wo;
-          const int py = static_cast<int>(fdiv(static_cast<uint32_t>(r2), a.div_wo));
-          const int px = r2 - py * a.Wo;
-          y = 2 * py + (pq >> 1);
-          xx = 2 * px + (pq & 1);
-        } else {
-          const int pix = quad * 4 + pq;
-          b = static_cast<int>(fdiv(static_cast<uint32_t>(pix), a.div_hw));
-          const int r2 = pix - b * HW;
-          y = static_cast<int>(fdiv(static_cast<uint32_t>(r2), a.div_w));
-          xx = r2 - y * a.W;
-        }
-        if constexpr (TAPS == 9) {
-          // tap kh*3 + kw reads (y + kh - 1, x + kw - 1)
-          const uint32_t vx = (xx > 0 ? 1u : 0u) | 2u | (xx + 1 < a.W ? 4u : 0u);
-          ok = (y > 0 ? vx : 0u) | (vx << 3) | (y + 1 < a.H ? vx << 6 : 0u);
-        } else {
-          ok = 1u;
-        }
-      }
-      const int c = swz(r, slot);
-      s_base[i] = static_cast<uint32_t>(t) * a.x_tstride_b +
-                  static_cast<uint32_t>(((b * a.H + y) * a.W + xx) * a.Cin) * 2u + (c & 3) * 16u;
-      s_ok[i] = ok;
-    } else {
-      const int n = kDmaRows * (wmn + (i - C::kAPer) * C::kGroupWaves) + lrow;
-      const int c = swz(n, slot);
-      s_base[i] = n0 + n < a.Cout
-                      ? static_cast<uint32_t>(n0 + n) * static_cast<uint32_t>(K) * 2u + c * 16u
-                      : kFar;
-    }
-  }
-
-  // every K group runs n_stages_g ring iterations (their barriers are
-  // shared); when the block's K stages do not split evenly over the groups,
-  // a group's last one lies past the block's range and is loaded as zeros
-  const int n_stages_g = (st_end - st_begin + KSPLIT - 1) / KSPLIT;
-  const int n_chunks = (a.T + 3) / 4;
-
-  // membrane state of the epilogue waves: [TM][TN][4 pixels]
-  float v[TM][TN][4];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[i][j][q] = 0.0f;
-
-  const int g_lane = lane >> 5, r_lane = lane & 31;
-  // epilogue columns and bias, filled after the first operand loads are on
-  // their way (the code before them runs once, from a cold instruction cache)
-  float bias_n[TN];
-  bool col_ok[TN];
-
-  // bias + LIF over the 4 steps of chunk tc (+ 2x2 OR) on the full K sum;
-  // the reset rule is a compile-time branch (kSoft) so that each neuron
-  // update is add, mul, mul, add, compare, select (+ sub when soft)
-  auto lif_epilogue = [&](const f32x16 (&acc)[TM][TN], int tc, auto soft_tag)
-                          __attribute__((always_inline)) {
-    constexpr bool kSoft = decltype(soft_tag)::value;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int quad = quad0 + (wm * TM + i) * 2 + g_lane;
-      if (quad >= a.n_quads) continue;
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        if (!col_ok[j]) continue;
-        const int n = n0 + (wn * TN + j) * 32 + r_lane;
-        // TAPS = 1 with POOL: the output keeps one column of every group of
-        // four adjacent columns (their OR), Cout / 4 columns per row
-        constexpr bool kColPool = POOL && TAPS == 1;
-        const int o_cols = kColPool ? a.Cout / 4 : a.Cout;
-        uint16_t* o = a.out + static_cast<int64_t>(tc) * 4 * a.o_tstride +
-                      (POOL && !kColPool ? static_cast<int64_t>(quad) * a.Cout + n
-                                         : static_cast<int64_t>(quad) * 4 * o_cols +
-                                               (kColPool ? n / 4 : n));
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if (tc * 4 + t >= a.T) break;
-          bool any = false;
-          bool sp[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float u = __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]);
-            const float h = __fadd_rn(__fmul_rn(a.decay, v[i][j][q]), __fmul_rn(a.in_scale, u));
-            const bool s = h >= a.vth;
-            if constexpr (kSoft) v[i][j][q] = s ? __fsub_rn(h, a.vth) : h;
-            else v[i][j][q] = s ? a.v_reset : h;
-            sp[q] = s;
-            any = any || s;
-          }
-          if constexpr (kColPool) {
-            // lanes 4k..4k+3 hold adjacent columns of the same rows: OR the
-            // 4 pixels' spikes (bit q) over the quad with two DPP exchanges
-            uint32_t m = (sp[0] ? 1u : 0u) | (sp[1] ? 2u : 0u) | (sp[2] ? 4u : 0u) | (sp[3] ? 8u : 0u);
-            m |= quad_dpp<0xB1>(m);  // lane ^ 1
-            m |= quad_dpp<0x4E>(m);  // lane ^ 2
-            if ((r_lane & 3) == 0) {
-#pragma unroll
-              for (int q = 0; q < 4; ++q) o[q * o_cols] = spike_bf16(((m >> q) & 1u) != 0);
-            }
-          } else if constexpr (POOL) {
-            o[0] = spike_bf16(any);
-          } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) o[q * a.Cout] = spike_bf16(sp[q]);
-          }
-          o += a.o_tstride;
-        }
-      }
-    }
-  };
-  // the LIF epilogue, or the fp32 pre-activations; run by the kg == 0 waves
-  // (both lambdas are forced inline: a call would move the accumulators to scratch)
-  auto epilogue = [&](const f32x16 (&acc)[TM][TN], int tc) __attribute__((always_inline)) {
-    if constexpr (MODE == MODE_PREACT) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int quad = quad0 + (wm * TM + i) * 2 + g_lane;
-        if (quad >= a.n_quads) continue;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          if (!col_ok[j]) continue;
-          const int n = n0 + (wn * TN + j) * 32 + r_lane;
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const int tg = tc * 4 + t;
-              if (tg < a.T) {
-                const int64_t p = static_cast<int64_t>(quad) * 4 + q;
-                a.pre[tg * a.o_tstride + p * a.Cout + n] = __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]);
-              }
-            }
-        }
-      }
-    } else if constexpr (MODE == MODE_MEAN) {
-      // running sum over the steps in v (one chunk of 4 at a time), written
-      // as sum / T after the last chunk
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int quad = quad0 + (wm * TM + i) * 2 + g_lane;
-        if (quad >= a.n_quads) continue;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          if (!col_ok[j]) continue;
-          const int n = n0 + (wn * TN + j) * 32 + r_lane;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-              if (tc * 4 + t < a.T)
-                v[i][j][q] = __fadd_rn(v[i][j][q], __fadd_rn(acc[i][j][q * 4 + t], bias_n[j]));
-            if (tc == n_chunks - 1)
-              a.pre[(static_cast<int64_t>(quad) * 4 + q) * a.Cout + n] =
-                  __fdiv_rn(v[i][j][q], static_cast<float>(a.T));
-          }
-        }
-      }
-    } else if (a.soft_reset) {
-      lif_epilogue(acc, tc, std::true_type{});
-    } else {
-      lif_epilogue(acc, tc, std::false_type{});
-    }
-  };
-
-  for (int tc = 0; tc < n_chunks; ++tc) {
-    // Source offsets of this lane's A segments for the tap pair (tap_lo,
-    // tap_hi) of the stage last prepared: kFar where the row, the step or
-    // the tap's source pixel does not exist.  A stage then costs one add
-    // per segment; the offsets are rebuilt only when the tap pair changes.
-    const bool t_ok = tc * 4 + (lrow & 3) < a.T;
-    const uint32_t chunk_off = static_cast<uint32_t>(tc) * 4u * a.x_tstride_b;
-    uint32_t a_off[C::kAPer];
-#pragma unroll
-    for (int i = 0; i < C::kAPer; ++i) a_off[i] = kFar;
-    int cur_lo = -1, cur_hi = -1;
-
-    // wave-uniform addressing of group-local stage sl
-    struct StageAddr {
-      bool live;        // a stage of the ring loop (later slots are not loaded)
-      bool zero_b;      // B reads zeros: a stage past the block's K range
-      bool tail;        // the last stage of K % 64 == 32: upper half past K
-      uint32_t da, db;  // A: chunk + channel bytes of the lower half; B: bytes of k0
-    };
-    auto prepare = [&](int sl) {
-      StageAddr p;
-      const int sg = st_begin + sl * KSPLIT + kg;
-      p.live = sl < n_stages_g;
-      p.zero_b = sg >= st_end;
-      const uint32_t k0 = p.zero_b ? 0u : static_cast<uint32_t>(sg * kKS);
-      const int tap_lo = static_cast<int>(fdiv(k0, a.div_cin));
-      const int cin_lo = static_cast<int>(k0) - tap_lo * a.Cin;
-      const bool wrap = cin_lo + 32 >= a.Cin;  // upper half starts the next tap
-      const int tap_hi = tap_lo + (wrap ? 1 : 0);
-      p.da = chunk_off + static_cast<uint32_t>(cin_lo) * 2u;
-      p.db = k0 * 2u;
-      p.tail = static_cast<int>(k0) + 32 >= K;
-      if (p.live && p.zero_b) {  // (rare) every A offset past the end as well
-        cur_lo = cur_hi = -1;
-        p.da = 0;
-#pragma unroll
-        for (int i = 0; i < C::kAPer; ++i) a_off[i] = kFar;
-      } else if (p.live && (tap_lo != cur_lo || tap_hi != cur_hi)) {
-        cur_lo = tap_lo;
-        cur_hi = tap_hi;
-        // byte delta of each half's source pixel, relative to p.da; the upper
-        // half sits 32 channels on, or at channel cin_lo + 32 - Cin of the
-        // next tap (a tap past the last has no ok bit: zeros)
-        const int32_t del_lo = (tap_dy<TAPS>(tap_lo) * a.W + tap_dx<TAPS>(tap_lo)) * a.Cin * 2;
-        const int32_t del_hi = (tap_dy<TAPS>(tap_hi) * a.W + tap_dx<TAPS>(tap_hi)) * a.Cin * 2 +
-                               64 - (wrap ? 2 * a.Cin : 0);
-#pragma unroll
-        for (int i = 0; i < C::kAPer; ++i) {
-          const uint32_t h = h0 ^ static_cast<uint32_t>((wmn + i * C::kGroupWaves) & 1);
-          const int tap = h ? tap_hi : tap_lo;
-          const bool ok = t_ok && ((s_ok[i] >> tap) & 1u);
-          a_off[i] = ok ? s_base[i] + static_cast<uint32_t>(h ? del_hi : del_lo) : kFar;
-        }
-      }
-      return p;
-    };
-    // enqueue the direct global->LDS load of segment i of a stage.  A ring
-    // slot past the loop is loaded too (never read; its offsets stay inside
-    // the operands or read zeros): a branch around each load cost more than
-    // the loads, and the waits stay conservative
-    auto issue_seg = [&](const StageAddr& p, int i, int buf) {
-      unsigned char* stage = smem + buf * C::kStageBytes;
-      if (i < C::kAPer) {  // resolved at compile time
-        const int q = wmn + i * C::kGroupWaves;
-        // (the offset goes through a variable: with the sum written in the
-        // call, hipcc's host pass drops the kernel's launch stub)
-        const uint32_t off = a_off[i] + p.da;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            xr, (lds_ptr_t)(stage + (kg * C::BM + kDmaRows * q) * kRowBytes), 16, off, 0, 0, 0);
-      } else {
-        const int q = wmn + (i - C::kAPer) * C::kGroupWaves;
-        const bool upper = (h0 ^ static_cast<uint32_t>(q & 1)) != 0;
-        const uint32_t off = (p.zero_b || (p.tail && upper)) ? kFar : s_base[i] + p.db;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            wr, (lds_ptr_t)(stage + (KSPLIT * C::BM + kg * C::BN + kDmaRows * q) * kRowBytes),
-            16, off, 0, 0, 0);
-      }
-    };
-
-    // a loop, not unrolled: this code runs once per launch from a cold
-    // instruction cache, so one copy of it is fetched instead of NBUF-1
-#pragma nounroll
-    for (int p = 0; p < C::kBuf - 1; ++p) {
-      const StageAddr sp = prepare(p);
-#pragma unroll
-      for (int i = 0; i < C::kSegPer; ++i) issue_seg(sp, i, p);
-    }
-    // set-up that no load waits for
-    if (tc == 0) {
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = n0 + (wn * TN + j) * 32 + r_lane;
-        col_ok[j] = n < a.Cout;
-        bias_n[j] = (a.bias && col_ok[j]) ? a.bias[n] : 0.0f;
-      }
-    }
-    f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-    constexpr int kSlices = kKS / 16;
-    int buf = 0;
-    // addressing of the stage the next iteration loads; prepared at the end
-    // of the previous iteration, so that after each barrier the fragment
-    // reads issue at once instead of behind the scalar stage arithmetic
-    StageAddr sp = prepare(C::kBuf - 1);
-    for (int s = 0; s < n_stages_g; ++s) {
-      // this wave's loads of stage s are done once at most the later
-      // stages' loads are outstanding; the barrier publishes every wave's
-      // loads and retires the reads of the buffer refilled next
-      wait_stages_barrier<C::kSegPer, C::kBuf - 2>(n_stages_g - 1 - s);
-      const int nbuf = buf == 0 ? C::kBuf - 1 : buf - 1;
-
-      const unsigned char* st = smem + buf * C::kStageBytes;
-      const uint16_t* sa = reinterpret_cast<const uint16_t*>(st) + (kg * C::BM + wm * TM * 32 + r_lane) * kRow;
-      const uint16_t* sb = reinterpret_cast<const uint16_t*>(st) +
-                           (KSPLIT * C::BM + kg * C::BN + wn * TN * 32 + r_lane) * kRow;
-      auto read = [&](bf16x8 (&fa)[TM], bf16x8 (&fb)[TN], int kk) {
-        // tile rows start at multiples of 32, so the swizzle depends on r_lane only
-        const int ch = swz(r_lane, kk * 2 + g_lane) * 8;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kRow + ch);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRow + ch);
-      };
-      // software pipeline over the k-slices: the reads of slice kk+1 and a
-      // share of the next stage's loads are in flight while slice kk's MFMAs
-      // run (the compiler's own interleaving measured 3-6% faster than
-      // scheduling barriers around each MFMA group)
-      bf16x8 fa[2][TM], fb[2][TN];
-      read(fa[0], fb[0], 0);
-#pragma unroll
-      for (int kk = 0; kk < kSlices; ++kk) {
-        if (kk + 1 < kSlices) read(fa[(kk + 1) & 1], fb[(kk + 1) & 1], kk + 1);
-#pragma unroll
-        for (int i = 0; i < C::kSegPer; ++i)
-          if (i % kSlices == kk) issue_seg(sp, i, nbuf);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
-      }
-      sp = prepare(s + C::kBuf);
-      buf = buf + 1 == C::kBuf ? 0 : buf + 1;
-    }
-    // every wave is done reading the ring before LDS is reused
-    wait_vmcnt_barrier<0>();
-
-    // ---- split-K reduction through LDS ----------------------------------
-    if constexpr (KSPLIT > 1) {
-      float* red = reinterpret_cast<float*>(smem);
-      if (kg > 0) {
-        float* dst = red + ((kg - 1) * WM * WN + wmn) * TM * TN * 16 * 64;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) dst[((i * TN + j) * 16 + e) * 64 + lane] = acc[i][j][e];
-      }
-      __syncthreads();
-      if (kg == 0) {
-#pragma unroll
-        for (int gg = 1; gg < KSPLIT; ++gg) {
-          const float* src = red + ((gg - 1) * WM * WN + wmn) * TM * TN * 16 * 64;
-#pragma unroll
-          for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-              for (int e = 0; e < 16; ++e) acc[i][j][e] += src[((i * TN + j) * 16 + e) * 64 + lane];
-        }
-      }
-      __syncthreads();
-    }
-
-    if (kg == 0) {
-      if (a.splits == 1) {
-        epilogue(acc, tc);
-      } else {
-        // this block's partial sums: 16-byte pieces, system-coherent (written
-        // through to memory, past this XCD's L2)
-        const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-            a.partials + (static_cast<int64_t>(mn) * a.splits + split) * n_chunks * (C::BM * C::BN),
-            0, -1, kRsrcWord3);
-        const uint32_t voff = static_cast<uint32_t>(tc * (C::BM * C::BN) + wmn * kPartFloats) * 4u +
-                              static_cast<uint32_t>(lane) * 16u;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const i32x4 v = {__float_as_int(acc[i][j][4 * q]), __float_as_int(acc[i][j][4 * q + 1]),
-                               __float_as_int(acc[i][j][4 * q + 2]), __float_as_int(acc[i][j][4 * q + 3])};
-              __builtin_amdgcn_raw_buffer_store_b128(v, pr, voff + ((i * TN + j) * 4 + q) * 1024, 0,
-                                                     kSystemCoherent);
-            }
-      }
-    }
-  }
-
-  // ---- cross-block split-K: the last block of a tile reduces and fires -----
-  if (a.splits > 1) {
-    // The partials were stored write-through and are read back with
-    // system-coherent loads, so no cache-wide fence is needed (an agent-scope
-    // fence writes back and invalidates the whole L2 of the XCD): each wave
-    // waits for its stores to be acknowledged, then one ticket per block.
-    // The operand ring is idle now; its first word carries the ticket result.
-    volatile unsigned int* s_last = reinterpret_cast<volatile unsigned int*>(smem);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0)
-      *s_last = __hip_atomic_fetch_add(a.tickets + mn, 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT) ==
-                static_cast<unsigned int>(a.splits - 1);
-    __syncthreads();
-    if (!*s_last) return;
-    if (kg == 0) {
-      // the tile's partial sums, read back with system-coherent 16-byte loads
-      const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-          a.partials + static_cast<int64_t>(mn) * a.splits * n_chunks * (C::BM * C::BN), 0, -1,
-          kRsrcWord3);
-      const uint32_t split_bytes = static_cast<uint32_t>(n_chunks * (C::BM * C::BN)) * 4u;
-      auto load_part = [&](f32x16 (&dst)[TM][TN], uint32_t voff) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-                  pr, voff + ((i * TN + j) * 4 + q) * 1024, 0, kSystemCoherent);
-#pragma unroll
-              for (int c = 0; c < 4; ++c) dst[i][j][4 * q + c] = __int_as_float(v[c]);
-            }
-      };
-      for (int tc = 0; tc < n_chunks; ++tc) {
-        const uint32_t voff = static_cast<uint32_t>(tc * (C::BM * C::BN) + wmn * kPartFloats) * 4u +
-                              static_cast<uint32_t>(lane) * 16u;
-        f32x16 acc[TM][TN];
-        load_part(acc, voff);
-        for (int sp = 1; sp < a.splits; ++sp) {  // fixed summation order
-          f32x16 part[TM][TN];
-          load_part(part, voff + sp * split_bytes);
-#pragma unroll
-          for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
-        }
-        epilogue(acc, tc);
-      }
-    }
-    if (tid == 0)  // ready for the next launch
-      __hip_atomic_store(a.tickets + mn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
-template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int MODE, int TAPS>
-int launch_cfg(const ConvArgs& a, hipStream_t stream) {
-  using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF>;
-  const int64_t per_xcd = (static_cast<int64_t>(a.tiles_m) * a.tiles_n * a.splits + 7) / 8;
-  if (per_xcd * 8 > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
-  hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, NBUF, POOL, MODE, TAPS>),
-                     dim3(static_cast<unsigned>(per_xcd * 8)), dim3(C::kThreads), 0, stream, a);
-  return launch_status();
-}
 
 constexpr int kNumTiles = 29;
 struct TileShape { int bm, bn; };
@@ -773,10 +118,6 @@ void auto_cfg_split(const ConvArgs& a, int* cfg, int* splits) {
 constexpr int64_t kMaxTickets = 65536;
 constexpr int64_t kTicketBytes = kMaxTickets * 4;
 
-struct Plan {
-  int cfg, splits, stages_per_split, tiles_m, tiles_n;
-  int64_t ticket_bytes, ws_bytes;
-};
 
 int make_plan(const ConvArgs& a, int tile_hint, int splits_hint, bool allow_split, Plan* p) {
   if (tile_hint >= kNumTiles || splits_hint < 0) return SNNK_EINVAL;
@@ -810,58 +151,6 @@ int make_plan(const ConvArgs& a, int tile_hint, int splits_hint, bool allow_spli
     p->ws_bytes = p->ticket_bytes + mn * p->splits * n_chunks * ts.bm * ts.bn * 4;
   }
   return SNNK_OK;
-}
-
-template <bool POOL, int MODE, int TAPS>
-int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) {
-  ConvArgs a = a0;
-  a.tiles_m = p.tiles_m;
-  a.tiles_n = p.tiles_n;
-  a.div_tiles_m = make_fastdiv(static_cast<uint32_t>(std::max(1, p.tiles_m)));
-  a.div_tiles_n = make_fastdiv(static_cast<uint32_t>(std::max(1, p.tiles_n)));
-  a.splits = p.splits;
-  a.stages_per_split = p.stages_per_split;
-  a.tickets = static_cast<unsigned int*>(workspace);
-  a.partials = p.splits > 1
-      ? reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + p.ticket_bytes) : nullptr;
-  //                               WM WN TM TN KS NBUF           block tile, LDS
-  switch (p.cfg) {
-    case 0: return launch_cfg<2, 2, 2, 4, 1, 3, POOL, MODE, TAPS>(a, s);   // 128 x 256, 144 KB
-    case 1: return launch_cfg<4, 1, 2, 2, 1, 2, POOL, MODE, TAPS>(a, s);   // 256 x 64, 80 KB
-    case 2: return launch_cfg<2, 2, 2, 2, 1, 2, POOL, MODE, TAPS>(a, s);   // 128 x 128, 64 KB
-    case 3: return launch_cfg<2, 2, 1, 2, 1, 3, POOL, MODE, TAPS>(a, s);   // 64 x 128, 72 KB
-    case 4: return launch_cfg<1, 1, 1, 1, 4, 3, POOL, MODE, TAPS>(a, s);   // 32 x 32 split-K 4, 96 KB
-    case 5: return launch_cfg<1, 2, 1, 2, 2, 2, POOL, MODE, TAPS>(a, s);   // 32 x 128 split-K 2, 80 KB
-    case 6: return launch_cfg<1, 1, 1, 1, 8, 2, POOL, MODE, TAPS>(a, s);   // 32 x 32 split-K 8, 128 KB
-    case 7: return launch_cfg<1, 1, 1, 2, 4, 2, POOL, MODE, TAPS>(a, s);   // 32 x 64 split-K 4, 96 KB
-    case 8: return launch_cfg<1, 2, 1, 2, 4, 2, POOL, MODE, TAPS>(a, s);   // 32 x 128 split-K 4, 160 KB
-    case 9: return launch_cfg<2, 2, 2, 2, 2, 2, POOL, MODE, TAPS>(a, s);   // 128 x 128 split-K 2, 128 KB
-    case 10: return launch_cfg<4, 1, 1, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 128 x 64, 72 KB
-    case 11: return launch_cfg<2, 2, 2, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 128 x 128, 96 KB
-    case 12: return launch_cfg<4, 1, 1, 2, 1, 4, POOL, MODE, TAPS>(a, s);  // 128 x 64, 96 KB
-    case 13: return launch_cfg<1, 1, 1, 2, 2, 3, POOL, MODE, TAPS>(a, s);  // 32 x 64 split-K 2, 72 KB
-    case 14: return launch_cfg<4, 2, 2, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 256 x 128, 144 KB
-    case 15: return launch_cfg<2, 2, 2, 2, 1, 4, POOL, MODE, TAPS>(a, s);  // 128 x 128, 128 KB
-    case 16: return launch_cfg<2, 2, 1, 2, 1, 4, POOL, MODE, TAPS>(a, s);  // 64 x 128, 96 KB
-    case 17: return launch_cfg<4, 1, 1, 2, 1, 5, POOL, MODE, TAPS>(a, s);  // 128 x 64, 120 KB
-    case 18: return launch_cfg<1, 2, 1, 2, 2, 3, POOL, MODE, TAPS>(a, s);  // 32 x 128 split-K 2, 120 KB
-    // four-wave and two-wave blocks with 128 x 64 / 64 x 128 per wave (fewer
-    // LDS fragment reads per MFMA than the 64 x 64 waves), and the 8-wave
-    // 128 x 256 transpose of 14
-    case 19: return launch_cfg<2, 2, 4, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 256 x 128, 144 KB
-    case 20: return launch_cfg<2, 2, 2, 4, 1, 3, POOL, MODE, TAPS>(a, s);  // 128 x 256, 144 KB
-    case 21: return launch_cfg<2, 4, 2, 2, 1, 3, POOL, MODE, TAPS>(a, s);  // 128 x 256, 144 KB
-    case 22: return launch_cfg<2, 1, 4, 2, 1, 2, POOL, MODE, TAPS>(a, s);  // 256 x 64, 80 KB
-    case 23: return launch_cfg<1, 2, 4, 2, 1, 2, POOL, MODE, TAPS>(a, s);  // 128 x 128, 64 KB
-    case 24: return launch_cfg<2, 1, 2, 4, 1, 2, POOL, MODE, TAPS>(a, s);  // 128 x 128, 64 KB
-    // deeper rings (4-5 stages) for the layers that stream their weights
-    // from memory: more stages in flight per block hide the longer latency
-    case 25: return launch_cfg<1, 1, 1, 1, 4, 5, POOL, MODE, TAPS>(a, s);  // 32 x 32 split-K 4, 160 KB
-    case 26: return launch_cfg<1, 1, 1, 2, 2, 5, POOL, MODE, TAPS>(a, s);  // 32 x 64 split-K 2, 120 KB
-    case 27: return launch_cfg<2, 2, 1, 2, 1, 5, POOL, MODE, TAPS>(a, s);  // 64 x 128, 120 KB
-    case 28: return launch_cfg<1, 2, 1, 2, 2, 4, POOL, MODE, TAPS>(a, s);  // 32 x 128 split-K 2, 160 KB
-    default: return SNNK_EINVAL;
-  }
 }
 
 // Validates a conv call and fills ConvArgs (no launch).
@@ -947,22 +236,48 @@ int linear_args(const uint16_t* x, const uint16_t* w, const float* bias, uint16_
   return SNNK_OK;
 }
 
+// Activation formats of the _act entry points: x read as packed words
+// (x_bytes shrinks to the packed size; kernel offsets stay in bf16 bytes and
+// are shifted down by 4 at the load), spikes written as packed words
+// (o_tstride in words).  Packed words need 4-byte alignment.
+int apply_act_formats(ConvArgs* a, const void* x, const void* out, int32_t x_fmt, int32_t out_fmt,
+                      bool* packed_in) {
+  if ((x_fmt != SNNK_ACT_BF16 && x_fmt != SNNK_ACT_BITS) ||
+      (out_fmt != SNNK_ACT_BF16 && out_fmt != SNNK_ACT_BITS))
+    return SNNK_EINVAL;
+  if (x == nullptr || out == nullptr) return SNNK_EINVAL;
+  *packed_in = x_fmt == SNNK_ACT_BITS;
+  if (!aligned(x, *packed_in ? 4 : 16) || !aligned(out, out_fmt == SNNK_ACT_BITS ? 4 : 2))
+    return SNNK_EALIGN;
+  if (*packed_in) a->x_bytes /= 16;  // bf16 bytes are a multiple of 64
+  if (out_fmt == SNNK_ACT_BITS) {
+    a->bits_out = 1;
+    a->o_tstride /= 32;
+  }
+  return SNNK_OK;
+}
+
 template <int TAPS>
 int run(const ConvArgs& a, bool pool, int tile_hint, int splits, bool allow_split, void* ws,
-        int64_t ws_bytes, hipStream_t s, bool mean = false) {
+        int64_t ws_bytes, hipStream_t s, bool mean = false, bool packed_in = false) {
   if (a.T == 0 || a.n_quads == 0) return SNNK_OK;
   Plan p;
   int st = make_plan(a, tile_hint, splits, allow_split, &p);
   if (st != SNNK_OK) return st;
   if (p.ws_bytes > 0 && (ws == nullptr || ws_bytes < p.ws_bytes)) return SNNK_EWORKSPACE;
   if (p.ws_bytes > 0 && !aligned(ws, 256)) return SNNK_EALIGN;
-  if constexpr (TAPS == 1) {
-    if (mean) return dispatch<false, MODE_MEAN, 1>(a, p, ws, s);
-    if (pool) return dispatch<true, MODE_LIF, 1>(a, p, ws, s);  // OR of column groups of 4
+  if (packed_in || a.bits_out) {
+    // LIF variants only; the column-pooled Linear keeps bf16 spikes
+    if (mean || a.pre != nullptr || (TAPS == 1 && pool)) return SNNK_EUNSUPPORTED;
+    if (packed_in) return dispatch_packed(a, p, ws, s, pool, TAPS);
   }
-  if (a.pre != nullptr) return dispatch<false, MODE_PREACT, TAPS>(a, p, ws, s);
-  if (pool) return dispatch<true, MODE_LIF, TAPS>(a, p, ws, s);
-  return dispatch<false, MODE_LIF, TAPS>(a, p, ws, s);
+  if constexpr (TAPS == 1) {
+    if (mean) return dispatch<false, MODE_MEAN, 1, false>(a, p, ws, s);
+    if (pool) return dispatch<true, MODE_LIF, 1, false>(a, p, ws, s);  // OR of column groups of 4
+  }
+  if (a.pre != nullptr) return dispatch<false, MODE_PREACT, TAPS, false>(a, p, ws, s);
+  if (pool) return dispatch<true, MODE_LIF, TAPS, false>(a, p, ws, s);
+  return dispatch<false, MODE_LIF, TAPS, false>(a, p, ws, s);
 }
 
 }  // namespace
@@ -1158,4 +473,45 @@ extern "C" int64_t snnk_linear_bias_lif_ws_size(int64_t T, int64_t R, int64_t K,
   Plan p;
   st = make_plan(a, tile_hint, splits, true, &p);
   return st != SNNK_OK ? st : p.ws_bytes;
+}
+
+extern "C" int snnk_conv3x3_bn_lif_act(const void* x, int32_t x_fmt, const uint16_t* w,
+                                       const float* bias, void* spikes_out, int32_t out_fmt,
+                                       int64_t T, int64_t B, int64_t H, int64_t W, int64_t Cin,
+                                       int64_t Cout, int32_t pool, float decay, float in_scale,
+                                       float v_threshold, float v_reset, int32_t soft_reset,
+                                       int32_t tile_hint, int32_t splits, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  if (T == 0 || B == 0 || H == 0 || W == 0) return (T < 0 || B < 0 || H < 0 || W < 0) ? SNNK_EINVAL : SNNK_OK;
+  if (w == nullptr || !aligned(w, 16)) return w == nullptr ? SNNK_EINVAL : SNNK_EALIGN;
+  ConvArgs a;
+  int st = conv_args(static_cast<const uint16_t*>(x), w, bias, static_cast<uint16_t*>(spikes_out),
+                     nullptr, T, B, H, W, Cin, Cout, pool, decay, in_scale, v_threshold, v_reset,
+                     soft_reset, false, &a);
+  if (st != SNNK_OK) return st;
+  bool packed_in = false;
+  st = apply_act_formats(&a, x, spikes_out, x_fmt, out_fmt, &packed_in);
+  if (st != SNNK_OK) return st;
+  return run<9>(a, pool != 0, tile_hint, splits, true, workspace, workspace_bytes,
+                static_cast<hipStream_t>(stream), false, packed_in);
+}
+
+extern "C" int snnk_linear_bias_lif_act(const void* x, int32_t x_fmt, const uint16_t* w,
+                                        const float* bias, void* spikes_out, int32_t out_fmt,
+                                        int64_t T, int64_t R, int64_t K, int64_t N, float decay,
+                                        float in_scale, float v_threshold, float v_reset,
+                                        int32_t soft_reset, int32_t tile_hint, int32_t splits,
+                                        void* workspace, int64_t workspace_bytes, void* stream) {
+  if (T == 0 || R == 0) return (T < 0 || R < 0) ? SNNK_EINVAL : SNNK_OK;
+  if (w == nullptr || !aligned(w, 16)) return w == nullptr ? SNNK_EINVAL : SNNK_EALIGN;
+  ConvArgs a;
+  int st = linear_args(static_cast<const uint16_t*>(x), w, bias,
+                       static_cast<uint16_t*>(spikes_out), nullptr, T, R, K, N, decay, in_scale,
+                       v_threshold, v_reset, soft_reset, false, &a);
+  if (st != SNNK_OK) return st;
+  bool packed_in = false;
+  st = apply_act_formats(&a, x, spikes_out, x_fmt, out_fmt, &packed_in);
+  if (st != SNNK_OK) return st;
+  return run<1>(a, false, tile_hint, splits, true, workspace, workspace_bytes,
+                static_cast<hipStream_t>(stream), false, packed_in);
 }

@@ -24,6 +24,8 @@ F32, BF16, F16, U8, I32 = 0, 1, 2, 3, 4
 SPIKE_SAME, SPIKE_U8, SPIKE_BF16, SPIKE_BITS = 0, 1, 2, 3
 # threshold modes
 THR_SCALAR, THR_PER_CHANNEL, THR_PER_NEURON = 0, 1, 2
+# activation formats of the _act entry points
+ACT_BF16, ACT_BITS = 0, 1
 # binary GEMM algorithms
 BGEMM_AUTO, BGEMM_POPC, BGEMM_MFMA_I8, BGEMM_MFMA_F4 = 0, 1, 2, 3
 
@@ -97,6 +99,25 @@ PROTOTYPES: dict[str, list] = {
     "snnk_linear_bias_lif_ws": [
         _p, _p, _p,            # x, w, bias
         _p, _p,                # spikes_out, preact_out
+        _i64, _i64, _i64, _i64,  # T, R, K, N
+        _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
+        _i32, _i32,            # soft_reset, tile_hint
+        _i32, _p, _i64,        # splits, workspace, workspace_bytes
+        _p,                    # stream
+    ],
+    "snnk_conv3x3_bn_lif_act": [
+        _p, _i32, _p, _p,      # x, x_fmt, w, bias
+        _p, _i32,              # spikes_out, out_fmt
+        _i64, _i64, _i64, _i64,  # T, B, H, W
+        _i64, _i64, _i32,      # Cin, Cout, pool
+        _f32, _f32, _f32,      # decay, in_scale, v_threshold
+        _f32, _i32, _i32,      # v_reset, soft_reset, tile_hint
+        _i32, _p, _i64,        # splits, workspace, workspace_bytes
+        _p,                    # stream
+    ],
+    "snnk_linear_bias_lif_act": [
+        _p, _i32, _p, _p,      # x, x_fmt, w, bias
+        _p, _i32,              # spikes_out, out_fmt
         _i64, _i64, _i64, _i64,  # T, R, K, N
         _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
         _i32, _i32,            # soft_reset, tile_hint

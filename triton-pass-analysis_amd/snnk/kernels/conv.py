@@ -117,6 +117,55 @@ def _conv_call(x, w_prep, bias, out, pre, pool, decay, in_scale, v_threshold, v_
                   0 if ws is None else ws.numel(), _abi.stream(x.device))
 
 
+def _act_code(t: torch.Tensor) -> int:
+    """Activation format of a tensor: bf16 0/1 values or int32 packed words."""
+    if t.dtype == torch.bfloat16:
+        return _abi.ACT_BF16
+    if t.dtype == torch.int32:
+        return _abi.ACT_BITS
+    raise AssertionError(f"activations are bf16 0/1 or int32 packed words, not {t.dtype}")
+
+
+def conv3x3_bn_lif_act(x: torch.Tensor, w_prep: torch.Tensor, bias: torch.Tensor | None, *,
+                       pool: bool, decay: float, in_scale: float, v_threshold: float,
+                       v_reset: float = 0.0, soft_reset: bool = False, out_bits: bool = True,
+                       out: torch.Tensor | None = None, tile_hint: int = -1,
+                       splits: int | None = None) -> torch.Tensor:
+    """:func:`conv3x3_bn_lif_nhwc` with bit-packed activations on either side.
+
+    x: NHWC bf16 0/1 ``[T, B, H, W, Cin]``, or int32 packed words
+    ``[T, B, H, W, Cin // 32]`` (bit c%32 of word c//32, LSB first).  Returns
+    int32 words ``[T, B, Ho, Wo, Cout // 32]`` (``out_bits=True``) or bf16
+    ``[T, B, Ho, Wo, Cout]``.  The spikes are identical to the bf16 path's."""
+    assert x.is_cuda and x.ndim == 5 and x.is_contiguous()
+    x_fmt = _act_code(x)
+    T, B, H, W, Cx = x.shape
+    Cin = Cx * 32 if x_fmt == _abi.ACT_BITS else Cx
+    Cout = w_prep.shape[0]
+    assert w_prep.dtype == torch.bfloat16 and w_prep.shape == (Cout, 9 * Cin) \
+        and w_prep.is_contiguous() and w_prep.device == x.device
+    if bias is not None:
+        assert bias.dtype == torch.float32 and bias.numel() == Cout and bias.is_contiguous()
+    Ho, Wo = (H // 2, W // 2) if pool else (H, W)
+    shape = (T, B, Ho, Wo, Cout // 32 if out_bits else Cout)
+    dt = torch.int32 if out_bits else torch.bfloat16
+    if out is None:
+        out = torch.empty(shape, device=x.device, dtype=dt)
+    else:
+        assert out.shape == shape and out.dtype == dt and out.is_contiguous()
+    sp = 0 if splits is None else int(splits)
+    with torch.cuda.device(x.device):
+        nbytes = _abi.size_call("snnk_conv3x3_bn_lif_ws_size", T, B, H, W, Cin, Cout,
+                                1 if pool else 0, 0, int(tile_hint), sp)
+        ws = _workspace.get(x.device, nbytes)
+        _abi.call("snnk_conv3x3_bn_lif_act", x.data_ptr(), x_fmt, w_prep.data_ptr(),
+                  _abi.ptr(bias), out.data_ptr(), _abi.ACT_BITS if out_bits else _abi.ACT_BF16,
+                  T, B, H, W, Cin, Cout, 1 if pool else 0, float(decay), float(in_scale),
+                  float(v_threshold), float(v_reset), 1 if soft_reset else 0, int(tile_hint),
+                  sp, _abi.ptr(ws), 0 if ws is None else ws.numel(), _abi.stream(x.device))
+    return out
+
+
 def conv3x3_preact_nhwc(x: torch.Tensor, w_prep: torch.Tensor, bias: torch.Tensor | None,
                         *, tile_hint: int = -1, splits: int | None = None) -> torch.Tensor:
     """fp32 conv + bias, NHWC ``[T, B, H, W, Cout]`` (the membrane input, no LIF)."""
