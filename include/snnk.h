@@ -259,9 +259,12 @@ int64_t snnk_linear_bias_lif_ws_size(int64_t T, int64_t R, int64_t K, int64_t N,
  * packed bits (SNNK_ACT_BITS, 16x fewer bytes; the layout SNNK_SPIKE_BITS of
  * snnk_lif_forward gives for channels-last maps).  Packed x is expanded to
  * bf16 0/1 on its way into the MFMA operand stage; packed spikes are written
- * one 32-channel word per pixel and step.  Same tiling, results and
- * workspace contract as the _ws entry points (size it with *_ws_size, preact
- * = 0); LIF only.  Packed words need 4-byte alignment, bf16 x 16 bytes.
+ * one 32-channel word per pixel and step.  Same results and workspace
+ * contract as the _ws entry points; packed x has its own tile and split
+ * plan (size the workspace with the *_act_ws_size functions below); LIF
+ * only.  col_pool != 0 (Linear): the OR of each group of four adjacent output
+ * columns, as snnk_linear_bias_lif_pool4_ws, with bf16 spikes out.  Packed
+ * words need 4-byte alignment, bf16 x 16 bytes.
  *
  * Replaces the same layer pairs as snnk_conv3x3_bn_lif / snnk_linear_bias_lif,
  * with the bit-packed activation format of _pack_N
@@ -279,10 +282,19 @@ int snnk_conv3x3_bn_lif_act(const void* x, int32_t x_fmt, const uint16_t* w, con
                             void* stream);
 int snnk_linear_bias_lif_act(const void* x, int32_t x_fmt, const uint16_t* w, const float* bias,
                              void* spikes_out, int32_t out_fmt, int64_t T, int64_t R,
-                             int64_t K, int64_t N, float decay, float in_scale,
-                             float v_threshold, float v_reset, int32_t soft_reset,
-                             int32_t tile_hint, int32_t splits, void* workspace,
-                             int64_t workspace_bytes, void* stream);
+                             int64_t K, int64_t N, int32_t col_pool, float decay,
+                             float in_scale, float v_threshold, float v_reset,
+                             int32_t soft_reset, int32_t tile_hint, int32_t splits,
+                             void* workspace, int64_t workspace_bytes, void* stream);
+/* Workspace bytes of the _act calls (packed x has its own tile / split plan,
+ * so its workspace may differ from the bf16 one); col_pool as in
+ * snnk_linear_bias_lif_pool4_ws (bf16 spikes out). */
+int64_t snnk_conv3x3_bn_lif_act_ws_size(int64_t T, int64_t B, int64_t H, int64_t W,
+                                        int64_t Cin, int64_t Cout, int32_t pool, int32_t x_fmt,
+                                        int32_t tile_hint, int32_t splits);
+int64_t snnk_linear_bias_lif_act_ws_size(int64_t T, int64_t R, int64_t K, int64_t N,
+                                         int32_t x_fmt, int32_t col_pool, int32_t tile_hint,
+                                         int32_t splits);
 
 /*
  * snnk_linear_bias_lif_ws followed by an OR over each group of four adjacent
@@ -389,6 +401,18 @@ int snnk_conv3x3_image_lif(const float* image, const float* w, const float* bias
                            int64_t H, int64_t W, int64_t Cout, float decay,
                            float in_scale, float v_threshold, float v_reset,
                            int32_t soft_reset, void* stream);
+
+/*
+ * snnk_conv3x3_image_lif with a choice of spike format: SNNK_ACT_BF16 as
+ * above, or SNNK_ACT_BITS, packed words [T][B][H][W][Cout/32] (bit c%32 of
+ * word c/32; Cout % 32 == 0, 4-byte alignment), the input format of
+ * snnk_conv3x3_bn_lif_act.
+ */
+int snnk_conv3x3_image_lif_act(const float* image, const float* w, const float* bias,
+                               void* spikes_out, int32_t out_fmt, int64_t T, int64_t B,
+                               int64_t Cin, int64_t H, int64_t W, int64_t Cout, float decay,
+                               float in_scale, float v_threshold, float v_reset,
+                               int32_t soft_reset, void* stream);
 
 /*
  * Layout change [N][C][HW] -> [N][HW][C] with conversion to bf16

@@ -159,3 +159,19 @@ def test_lif_packed_words_feed_conv():
                               pool=False, out_bits=False, **LIF)
     b = kc.conv3x3_bn_lif_nhwc(s.to(DEV, torch.bfloat16), wp, bd, pool=False, **LIF)
     assert torch.equal(a.cpu(), b.cpu())
+
+
+@pytest.mark.parametrize("B,H,W,Cout", [(32, 32, 32, 64), (1, 32, 32, 64), (56, 32, 32, 64),
+                                        (3, 12, 10, 96), (2, 7, 9, 32)])
+def test_image_layer_packed_output(B, H, W, Cout):
+    """The image layer's packed words are its bf16 spikes, packed (all three
+    pixel-run widths: runs of 4 at B=56, 2 at B=32, 1 at odd widths)."""
+    g = torch.Generator().manual_seed(B + H)
+    img = torch.randn(B, 3, H, W, generator=g).to(DEV)
+    w = (torch.randn(Cout, 3, 3, 3, generator=g) * 0.6).to(DEV)
+    b = (torch.randn(Cout, generator=g) * 0.1).to(DEV)
+    bf = kc.conv3x3_image_lif(img, w, b, 4, **LIF).cpu()
+    words = kc.conv3x3_image_lif(img, w, b, 4, out_bits=True, **LIF).cpu()
+    assert words.dtype == torch.int32 and words.shape == (4, B, H, W, Cout // 32)
+    assert torch.equal(words, _pack(bf))
+    assert 0 < int(bf.float().sum()) < bf.numel()

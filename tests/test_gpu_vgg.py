@@ -198,3 +198,49 @@ def test_fused_pool_module_teacher_forced():
     trace = of.membrane_trace(y.cpu())
     agree, bad = _flips_ok(got.cpu(), want.cpu(), trace, True, 5e-2)
     assert agree >= 0.999 and not bad, agree
+
+
+def _unpack(words, C):
+    """int32 packed words [..., C // 32] -> float 0/1 [..., C] (bit c%32 of word c//32)."""
+    bits = (words.unsqueeze(-1) >> torch.arange(32, device=words.device)) & 1
+    return bits.reshape(*words.shape[:-1], C).float()
+
+
+@pytest.mark.parametrize("B,gain", [(32, 3.0), (1, 3.0), (56, 3.0)])
+def test_teacher_forced_layers_on_packed_bits(B, gain):
+    """The engine chains its conv layers on packed words: every conv layer fed
+    the oracle's input as words gives exactly the spikes of the bf16 path (and
+    so the same >= 99.9% agreement with the fp32 oracle)."""
+    from snnk.kernels.binary import pack_bits
+    eng = _engine(gain)
+    assert eng.bits_between_layers
+    rec = ov.forward_layers(ov.make_params(0, gain=gain), _image(B), T)
+    convs = iter(eng.convs)
+    n = 0
+    for i, r in enumerate(rec):
+        if r["kind"] != "conv":
+            continue
+        conv = next(convs)
+        x = to_nhwc_bf16(r["input"].to(DEV))
+        bf = conv.forward_nhwc(x).cpu().float()
+        got = conv.forward_nhwc(pack_bits(x, dim=-1), out_bits=True)
+        C = bf.shape[-1]
+        got = _unpack(got, C).cpu() if got.dtype == torch.int32 else got.cpu().float()
+        assert torch.equal(got, bf), f"layer {i}: packed path differs from bf16 path"
+        agree, bad = _flips_ok(got.permute(0, 1, 4, 2, 3), r["output"], r["trace"],
+                               r.get("pool", False), 2e-2)
+        assert agree >= 0.999 and not bad, f"layer {i}: agreement {agree}"
+        n += 1
+    assert n == 12
+
+
+def test_engine_bits_and_bf16_chains_agree():
+    """Same network, activations as packed words or as bf16 between layers:
+    identical logits (the formats carry the same spikes)."""
+    eng = _engine(3.0)
+    img = _image(32).to(DEV)
+    y_bits = eng(img).clone()
+    eng.bits_between_layers = False
+    y_bf16 = eng(img)
+    eng.bits_between_layers = True
+    assert torch.equal(y_bits, y_bf16)

@@ -119,11 +119,62 @@ constexpr int64_t kMaxTickets = 65536;
 constexpr int64_t kTicketBytes = kMaxTickets * 4;
 
 
-int make_plan(const ConvArgs& a, int tile_hint, int splits_hint, bool allow_split, Plan* p) {
+// Tile shape and split for packed-spike input, from sweeps of every (tile,
+// splits) pair over the VGG16 layers at batch 1, 32 and 56: with the A
+// operand 16x smaller in LDS, taller tiles and more K groups pay where the
+// bf16 rule picked small ones (VGG L4 at batch 32: 16.3 us with 128x128 tiles
+// and 2 K groups against 22.2 with 256x128; L2 at batch 56: 27.8 us with
+// 128x64 against 47.7 with 128x128).  Batch 1 keeps the bf16 rule.
+bool auto_cfg_packed(const ConvArgs& a, bool taps9, int* cfg, int* splits) {
+  const int64_t rows = static_cast<int64_t>(a.n_quads) * 16;
+  const int64_t K = static_cast<int64_t>(a.n_stages) * kKS;
+  const bool pool = a.Ho != a.H;
+  *splits = 1;
+  if (!taps9) {                                   // Linear (FC, dense 2x2 maps)
+    if (rows <= 64 || rows > 256) return false;
+    if (K >= 4096) { *cfg = rows <= 128 ? 7 : 12; *splits = rows <= 128 ? 2 : 3; return true; }
+    if (K >= 2048) { if (rows <= 128) return false; *cfg = 7; *splits = 2; return true; }
+    if (K <= 512) { *cfg = rows <= 128 ? 4 : 7; return true; }
+    return false;
+  }
+  if (rows >= 65536) {                            // VGG L2 at batch 32 / 56
+    if (a.Cout > 64) return false;
+    *cfg = pool && rows >= 196608 ? 10 : 1;
+    return true;
+  }
+  if (rows >= 32768) {                            // L3, L4
+    if (rows >= 49152) *cfg = pool ? 14 : 2;
+    else *cfg = pool ? 9 : 10;
+    return true;
+  }
+  if (rows >= 8192) {                             // L5 - L7
+    if (a.Cout >= 512) *cfg = rows >= 12288 ? 14 : 9;
+    else if (K <= 1152) *cfg = 10;
+    else if (rows >= 12288) *cfg = 9;
+    else *cfg = pool ? 5 : 12;
+    return true;
+  }
+  if (rows >= 2048) {                             // L8 - L10
+    if (K <= 1152) { *cfg = 4; return true; }
+    if (rows <= 2048) { *cfg = 7; return true; }
+    if (K <= 2304) { *cfg = 5; return true; }
+    *cfg = pool ? 10 : 12;
+    *splits = 2;
+    return true;
+  }
+  return false;
+}
+
+// packed_taps: 0 for bf16 x, else the kernel's taps (9: conv, 1: Linear)
+// with packed x, which has its own plan rule
+int make_plan(const ConvArgs& a, int tile_hint, int splits_hint, bool allow_split, Plan* p,
+              int packed_taps = 0) {
   if (tile_hint >= kNumTiles || splits_hint < 0) return SNNK_EINVAL;
   int auto_splits = 1;
   if (tile_hint >= 0) p->cfg = tile_hint;
-  else if (allow_split && splits_hint != 1) auto_cfg_split(a, &p->cfg, &auto_splits);
+  else if (packed_taps != 0 && allow_split && splits_hint != 1 &&
+           auto_cfg_packed(a, packed_taps == 9, &p->cfg, &auto_splits)) {
+  } else if (allow_split && splits_hint != 1) auto_cfg_split(a, &p->cfg, &auto_splits);
   else p->cfg = auto_cfg(a);
   const TileShape ts = kTile[p->cfg];
   p->tiles_m = (a.n_quads + ts.bm / 16 - 1) / (ts.bm / 16);
@@ -262,13 +313,13 @@ int run(const ConvArgs& a, bool pool, int tile_hint, int splits, bool allow_spli
         int64_t ws_bytes, hipStream_t s, bool mean = false, bool packed_in = false) {
   if (a.T == 0 || a.n_quads == 0) return SNNK_OK;
   Plan p;
-  int st = make_plan(a, tile_hint, splits, allow_split, &p);
+  int st = make_plan(a, tile_hint, splits, allow_split, &p, packed_in ? TAPS : 0);
   if (st != SNNK_OK) return st;
   if (p.ws_bytes > 0 && (ws == nullptr || ws_bytes < p.ws_bytes)) return SNNK_EWORKSPACE;
   if (p.ws_bytes > 0 && !aligned(ws, 256)) return SNNK_EALIGN;
   if (packed_in || a.bits_out) {
-    // LIF variants only; the column-pooled Linear keeps bf16 spikes
-    if (mean || a.pre != nullptr || (TAPS == 1 && pool)) return SNNK_EUNSUPPORTED;
+    // LIF variants only; the column-pooled Linear writes bf16 spikes
+    if (mean || a.pre != nullptr || (TAPS == 1 && pool && a.bits_out)) return SNNK_EUNSUPPORTED;
     if (packed_in) return dispatch_packed(a, p, ws, s, pool, TAPS);
   }
   if constexpr (TAPS == 1) {
@@ -498,20 +549,50 @@ extern "C" int snnk_conv3x3_bn_lif_act(const void* x, int32_t x_fmt, const uint1
 
 extern "C" int snnk_linear_bias_lif_act(const void* x, int32_t x_fmt, const uint16_t* w,
                                         const float* bias, void* spikes_out, int32_t out_fmt,
-                                        int64_t T, int64_t R, int64_t K, int64_t N, float decay,
-                                        float in_scale, float v_threshold, float v_reset,
-                                        int32_t soft_reset, int32_t tile_hint, int32_t splits,
-                                        void* workspace, int64_t workspace_bytes, void* stream) {
+                                        int64_t T, int64_t R, int64_t K, int64_t N,
+                                        int32_t col_pool, float decay, float in_scale,
+                                        float v_threshold, float v_reset, int32_t soft_reset,
+                                        int32_t tile_hint, int32_t splits, void* workspace,
+                                        int64_t workspace_bytes, void* stream) {
   if (T == 0 || R == 0) return (T < 0 || R < 0) ? SNNK_EINVAL : SNNK_OK;
   if (w == nullptr || !aligned(w, 16)) return w == nullptr ? SNNK_EINVAL : SNNK_EALIGN;
   ConvArgs a;
   int st = linear_args(static_cast<const uint16_t*>(x), w, bias,
                        static_cast<uint16_t*>(spikes_out), nullptr, T, R, K, N, decay, in_scale,
-                       v_threshold, v_reset, soft_reset, false, &a);
+                       v_threshold, v_reset, soft_reset, false, &a, col_pool != 0);
   if (st != SNNK_OK) return st;
   bool packed_in = false;
   st = apply_act_formats(&a, x, spikes_out, x_fmt, out_fmt, &packed_in);
   if (st != SNNK_OK) return st;
-  return run<1>(a, false, tile_hint, splits, true, workspace, workspace_bytes,
+  return run<1>(a, col_pool != 0, tile_hint, splits, true, workspace, workspace_bytes,
                 static_cast<hipStream_t>(stream), false, packed_in);
+}
+
+extern "C" int64_t snnk_conv3x3_bn_lif_act_ws_size(int64_t T, int64_t B, int64_t H, int64_t W,
+                                                   int64_t Cin, int64_t Cout, int32_t pool,
+                                                   int32_t x_fmt, int32_t tile_hint,
+                                                   int32_t splits) {
+  if (T == 0 || B == 0 || H == 0 || W == 0) return (T < 0 || B < 0 || H < 0 || W < 0) ? SNNK_EINVAL : 0;
+  if (x_fmt != SNNK_ACT_BF16 && x_fmt != SNNK_ACT_BITS) return SNNK_EINVAL;
+  ConvArgs a;
+  int st = conv_args(nullptr, nullptr, nullptr, nullptr, nullptr, T, B, H, W, Cin, Cout, pool,
+                     0.f, 0.f, 0.f, 0.f, 0, false, &a);
+  if (st != SNNK_OK) return st;
+  Plan p;
+  st = make_plan(a, tile_hint, splits, true, &p, x_fmt == SNNK_ACT_BITS ? 9 : 0);
+  return st != SNNK_OK ? st : p.ws_bytes;
+}
+
+extern "C" int64_t snnk_linear_bias_lif_act_ws_size(int64_t T, int64_t R, int64_t K, int64_t N,
+                                                    int32_t x_fmt, int32_t col_pool,
+                                                    int32_t tile_hint, int32_t splits) {
+  if (T == 0 || R == 0) return (T < 0 || R < 0) ? SNNK_EINVAL : 0;
+  if (x_fmt != SNNK_ACT_BF16 && x_fmt != SNNK_ACT_BITS) return SNNK_EINVAL;
+  ConvArgs a;
+  int st = linear_args(nullptr, nullptr, nullptr, nullptr, nullptr, T, R, K, N, 0.f, 0.f, 0.f,
+                       0.f, 0, false, &a, col_pool != 0);
+  if (st != SNNK_OK) return st;
+  Plan p;
+  st = make_plan(a, tile_hint, splits, true, &p, x_fmt == SNNK_ACT_BITS ? 1 : 0);
+  return st != SNNK_OK ? st : p.ws_bytes;
 }

@@ -7,9 +7,13 @@
 // per (pixel, channel) in fp32 on the VALU (K = 9*Cin is far too small for
 // MFMA) and the LIF recurrence runs T times on that constant current.
 // Cout % 8 == 0 and the folded weights (9*Cin*Cout fp32) fit 64 KB of LDS.
-// Output spikes go to NHWC bf16 [T][B][H][W][Cout] for the next MFMA layer.
+// Output spikes go to NHWC bf16 [T][B][H][W][Cout] for the next MFMA layer,
+// or (snnk_conv3x3_image_lif_act, SNNK_ACT_BITS) to packed words
+// [T][B][H][W][Cout/32].
 //
 // snnk_to_nhwc_bf16: [N][C][HW] (fp32/bf16/f16/u8) -> [N][HW][C] bf16.
+#include <type_traits>
+
 #include "snnk_common.h"
 
 namespace snnk {
@@ -32,7 +36,17 @@ namespace {
 constexpr int kImgG = 8;
 constexpr int kImgMaxLds = 64 * 1024;
 
-template <int P, int CC>
+// v of the lane CTRL names within each group of 4 lanes (DPP quad_perm)
+template <int CTRL>
+__device__ __forceinline__ uint32_t quad_lane(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+// BITS: spikes as packed words [T][B][H][W][Cout/32] (bit c%32 of word c/32):
+// the 4 lanes of a quad hold channel groups 4w..4w+3 of one pixel run
+// (Cout % 32 == 0 makes the groups per run a multiple of 4), so their 8-bit
+// spike sets OR into word w over two DPP exchanges.
+template <int P, int CC, bool BITS>
 __global__ __launch_bounds__(256) void conv_image_lif_kernel(
     const float* __restrict__ img, const float* __restrict__ w, const float* __restrict__ bias,
     uint16_t* __restrict__ out, int T, int n_pix, int Cin, int H, int W, int Cout, float decay,
@@ -129,8 +143,11 @@ __global__ __launch_bounds__(256) void conv_image_lif_kernel(
       v[j] = 0.0f;
     }
     uint16_t* o = out + static_cast<int64_t>(p + q) * Cout + n0;
+    uint32_t* ow = reinterpret_cast<uint32_t*>(out) + static_cast<int64_t>(p + q) * (Cout / 32) +
+                   n0 / 32;
     for (int t = 0; t < T; ++t) {
       uint32_t bits[kImgG / 2];
+      uint32_t byte = 0;
 #pragma unroll
       for (int j = 0; j < kImgG; ++j) {
         const float h = __fadd_rn(__fmul_rn(decay, v[j]), __fmul_rn(in_scale, u[j]));
@@ -139,8 +156,16 @@ __global__ __launch_bounds__(256) void conv_image_lif_kernel(
         const uint32_t sb = s ? 0x3F80u : 0u;
         if (j & 1) bits[j / 2] |= sb << 16;
         else bits[j / 2] = sb;
+        byte |= s ? 1u << j : 0u;
       }
-      *reinterpret_cast<u32x4*>(o + t * step) = u32x4{bits[0], bits[1], bits[2], bits[3]};
+      if constexpr (BITS) {
+        uint32_t wd = byte << (8 * ((n0 / kImgG) & 3));
+        wd |= quad_lane<0xB1>(wd);  // lane ^ 1
+        wd |= quad_lane<0x4E>(wd);  // lane ^ 2
+        if (((n0 / kImgG) & 3) == 0) ow[t * (step / 32)] = wd;
+      } else {
+        *reinterpret_cast<u32x4*>(o + t * step) = u32x4{bits[0], bits[1], bits[2], bits[3]};
+      }
     }
   }
 }
@@ -190,18 +215,21 @@ __global__ __launch_bounds__(256) void to_nhwc_kernel(const Raw* __restrict__ sr
 
 using namespace snnk;
 
-extern "C" int snnk_conv3x3_image_lif(const float* image, const float* w, const float* bias,
-                                      uint16_t* spikes_out, int64_t T, int64_t B, int64_t Cin,
-                                      int64_t H, int64_t W, int64_t Cout, float decay,
-                                      float in_scale, float v_threshold, float v_reset,
-                                      int32_t soft_reset, void* stream) {
+extern "C" int snnk_conv3x3_image_lif_act(const float* image, const float* w, const float* bias,
+                                          void* spikes_out, int32_t out_fmt, int64_t T,
+                                          int64_t B, int64_t Cin, int64_t H, int64_t W,
+                                          int64_t Cout, float decay, float in_scale,
+                                          float v_threshold, float v_reset, int32_t soft_reset,
+                                          void* stream) {
   if (T < 0 || B < 0 || Cin <= 0 || H < 0 || W < 0 || Cout <= 0) return SNNK_EINVAL;
+  if (out_fmt != SNNK_ACT_BF16 && out_fmt != SNNK_ACT_BITS) return SNNK_EINVAL;
   if (T == 0 || B == 0 || H == 0 || W == 0) return SNNK_OK;
   if (image == nullptr || w == nullptr || spikes_out == nullptr) return SNNK_EINVAL;
-  // channel groups of 8 are stored as 16-byte vectors; all folded weights
-  // must fit the kernel's LDS
+  const bool bits = out_fmt == SNNK_ACT_BITS;
+  // channel groups of 8 are stored as 16-byte vectors (packed: 32-channel
+  // words); all folded weights must fit the kernel's LDS
   const int64_t lds = Cin * 9 * Cout * 4;
-  if (Cout % kImgG != 0 || lds > kImgMaxLds) return SNNK_EUNSUPPORTED;
+  if (Cout % (bits ? 32 : kImgG) != 0 || lds > kImgMaxLds) return SNNK_EUNSUPPORTED;
   if (B * H * W > 0x7FFFFFFFll || B * H * W * Cin > (1ll << 40) ||
       T * B * H * W * Cout > (1ll << 40))
     return SNNK_EUNSUPPORTED;
@@ -217,16 +245,30 @@ extern "C" int snnk_conv3x3_image_lif(const float* image, const float* w, const 
   if (blocks > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
   // channel chunk: 3 for RGB-like inputs, else 4
   const bool c3 = Cin % 3 == 0;
-  auto kern = run == 4   ? (c3 ? conv_image_lif_kernel<4, 3> : conv_image_lif_kernel<4, 4>)
-              : run == 2 ? (c3 ? conv_image_lif_kernel<2, 3> : conv_image_lif_kernel<2, 4>)
-                         : (c3 ? conv_image_lif_kernel<1, 3> : conv_image_lif_kernel<1, 4>);
+  auto pick = [&](auto bits_tag) {
+    constexpr bool kBits = decltype(bits_tag)::value;
+    return run == 4   ? (c3 ? conv_image_lif_kernel<4, 3, kBits> : conv_image_lif_kernel<4, 4, kBits>)
+           : run == 2 ? (c3 ? conv_image_lif_kernel<2, 3, kBits> : conv_image_lif_kernel<2, 4, kBits>)
+                      : (c3 ? conv_image_lif_kernel<1, 3, kBits> : conv_image_lif_kernel<1, 4, kBits>);
+  };
+  auto kern = bits ? pick(std::true_type{}) : pick(std::false_type{});
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256),
                      static_cast<unsigned>(lds), static_cast<hipStream_t>(stream), image, w,
-                     bias, spikes_out, static_cast<int>(T), static_cast<int>(n_pix),
-                     static_cast<int>(Cin), static_cast<int>(H), static_cast<int>(W),
-                     static_cast<int>(Cout), decay, in_scale, v_threshold, v_reset,
-                     soft_reset ? 1 : 0);
+                     bias, static_cast<uint16_t*>(spikes_out), static_cast<int>(T),
+                     static_cast<int>(n_pix), static_cast<int>(Cin), static_cast<int>(H),
+                     static_cast<int>(W), static_cast<int>(Cout), decay, in_scale, v_threshold,
+                     v_reset, soft_reset ? 1 : 0);
   return launch_status();
+}
+
+extern "C" int snnk_conv3x3_image_lif(const float* image, const float* w, const float* bias,
+                                      uint16_t* spikes_out, int64_t T, int64_t B, int64_t Cin,
+                                      int64_t H, int64_t W, int64_t Cout, float decay,
+                                      float in_scale, float v_threshold, float v_reset,
+                                      int32_t soft_reset, void* stream) {
+  return snnk_conv3x3_image_lif_act(image, w, bias, spikes_out, SNNK_ACT_BF16, T, B, Cin, H, W,
+                                    Cout, decay, in_scale, v_threshold, v_reset, soft_reset,
+                                    stream);
 }
 
 extern "C" int snnk_to_nhwc_bf16(const void* src, int32_t src_dtype, uint16_t* dst, int64_t N,

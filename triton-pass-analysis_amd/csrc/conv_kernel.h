@@ -128,24 +128,32 @@ static_assert(offsetof(ConvArgs, x) / 64 == 0 && offsetof(ConvArgs, div_cin) / 6
                   sizeof(ConvArgs) <= 256,
               "the kernel touches one field per 64-byte line of ConvArgs");
 
-template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF>
+template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool PK = false>
 struct Cfg {
   static constexpr int kWaves = WM * WN * KSPLIT;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int BM = WM * TM * 32;
   static constexpr int BN = WN * TN * 32;
   static constexpr int kQuads = BM / 16;                    // quads per block
-  // operand stages arrive by 16-byte direct-to-LDS loads, one wave-wide
-  // load filling kDmaRows rows (1 KB); the WM*WN waves of a K group share them
-  static constexpr int kSegA = BM / kDmaRows;
+  // operand stages arrive by direct-to-LDS loads; the WM*WN waves of a K
+  // group share them.  B (and bf16 A): 16 bytes per lane, one wave-wide load
+  // filling kDmaRows rows (1 KB).  Packed A (PK): the stage's 64 bits of a
+  // row are 8 bytes, 4 per lane, one wave-wide load filling 32 rows.
+  static constexpr int kARowBytes = PK ? 8 : kRowBytes;
+  static constexpr int kARowsPerSeg = PK ? 32 : kDmaRows;
+  static constexpr int kSegA = BM / kARowsPerSeg;
   static constexpr int kSegB = BN / kDmaRows;
   static constexpr int kGroupWaves = WM * WN;
-  static_assert(kSegA % kGroupWaves == 0 && kSegB % kGroupWaves == 0,
+  static_assert((PK || kSegA % kGroupWaves == 0) && kSegB % kGroupWaves == 0,
                 "segments must split evenly over a group's waves");
-  static constexpr int kAPer = kSegA / kGroupWaves;  // per wave: A segments first,
-  static constexpr int kBPer = kSegB / kGroupWaves;  // then B segments
+  // per wave: A segments first, then B segments.  Packed A segments may not
+  // split evenly: the spare waves load a segment again (same bytes to the
+  // same place), so that every wave issues the same number of loads
+  static constexpr int kAPer = (kSegA + kGroupWaves - 1) / kGroupWaves;
+  static constexpr int kBPer = kSegB / kGroupWaves;
   static constexpr int kSegPer = kAPer + kBPer;
-  static constexpr int kStageBytes = KSPLIT * (BM + BN) * kRowBytes;
+  static constexpr int kAStageBytes = KSPLIT * BM * kARowBytes;  // B follows A in a stage
+  static constexpr int kStageBytes = kAStageBytes + KSPLIT * BN * kRowBytes;
   static constexpr int kBuf = NBUF;  // ring of operand stages in LDS
   static constexpr int kLdsBytes = kBuf * kStageBytes;
   static constexpr int kRedBytes = (KSPLIT - 1) * WM * WN * TM * TN * 16 * 64 * 4;
@@ -155,16 +163,16 @@ struct Cfg {
 
 __device__ __forceinline__ uint16_t spike_bf16(bool s) { return s ? 0x3F80u : 0u; }
 
-// 8 spikes (bits 0..7 of b, LSB first) -> 8 bf16 0/1 in four words: bits
-// 2i and 2i+1 are moved to bits 0 and 16 of word i, then scaled by 0x3F80
-// (bf16 1.0): one multiply of operands below 2^24.
+// 8 spikes (bits 0..7 of b, LSB first) -> 8 bf16 0/1 in four words.  With
+// e = b | b << 15, bits 2i and 2i+1 of b sit at bits 2i and 2i + 16 of e;
+// masking those two and multiplying by 0x3F80 >> 2i (exact: 0x3F80, bf16
+// 1.0, has seven trailing zeros) puts 0x3F80 in the halves they select.
+// Two VALU ops per word (the product stays below 2^24: a 24-bit multiply).
 __device__ __forceinline__ u32x4 bits_to_bf16x8(uint32_t b) {
+  const uint32_t e = b | (b << 15);
   u32x4 r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t x = (b >> (2 * i)) & 3u;
-    r[i] = ((x & 1u) | ((x & 2u) << 15)) * 0x3F80u;
-  }
+  for (int i = 0; i < 4; ++i) r[i] = (e & (0x10001u << (2 * i))) * (0x3F80u >> (2 * i));
   return r;
 }
 
@@ -185,7 +193,7 @@ template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int M
           bool PK>
 __global__ __launch_bounds__(64 * WM * WN * KSPLIT)
 void conv3x3_kernel(ConvArgs a) {
-  using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF>;
+  using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF, PK>;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::kSmem];
 
   const int tid = threadIdx.x;
@@ -262,8 +270,9 @@ void conv3x3_kernel(ConvArgs a) {
 #pragma unroll
   for (int i = 0; i < C::kSegPer; ++i) {
     if (i < C::kAPer) {
-      const int q = wmn + i * C::kGroupWaves;
-      const int r = kDmaRows * q + lrow;
+      // packed A: lane l takes row 32*q + l/2, half l%2 (its 4 bytes)
+      const int q = PK ? (wmn + i * C::kGroupWaves) % C::kSegA : wmn + i * C::kGroupWaves;
+      const int r = PK ? 32 * q + (lane >> 1) : kDmaRows * q + lrow;
       const int rr = r & 31;
       const int pq = rr >> 3, gr = (rr >> 2) & 1, t = rr & 3;
       const int quad = quad0 + (r >> 5) * 2 + gr;
@@ -295,7 +304,8 @@ void conv3x3_kernel(ConvArgs a) {
       }
       const int c = swz(r, slot);
       s_base[i] = static_cast<uint32_t>(t) * a.x_tstride_b +
-                  static_cast<uint32_t>(((b * a.H + y) * a.W + xx) * a.Cin) * 2u + (c & 3) * 16u;
+                  static_cast<uint32_t>(((b * a.H + y) * a.W + xx) * a.Cin) * 2u +
+                  (PK ? 0u : (c & 3) * 16u);
       s_ok[i] = ok;
     } else {
       const int n = kDmaRows * (wmn + (i - C::kAPer) * C::kGroupWaves) + lrow;
@@ -485,7 +495,9 @@ void conv3x3_kernel(ConvArgs a) {
     // tap_hi) of the stage last prepared: kFar where the row, the step or
     // the tap's source pixel does not exist.  A stage then costs one add
     // per segment; the offsets are rebuilt only when the tap pair changes.
-    const bool t_ok = tc * 4 + (lrow & 3) < a.T;
+    // (the step of this lane's A rows: row & 3, with row 8*q + l/8 -- or
+    // 32*q + l/2 for packed A)
+    const bool t_ok = tc * 4 + ((PK ? lane >> 1 : lrow) & 3) < a.T;
     const uint32_t chunk_off = static_cast<uint32_t>(tc) * 4u * a.x_tstride_b;
     uint32_t a_off[C::kAPer];
 #pragma unroll
@@ -528,26 +540,14 @@ void conv3x3_kernel(ConvArgs a) {
                                64 - (wrap ? 2 * a.Cin : 0);
 #pragma unroll
         for (int i = 0; i < C::kAPer; ++i) {
-          const uint32_t h = h0 ^ static_cast<uint32_t>((wmn + i * C::kGroupWaves) & 1);
+          const uint32_t h = PK ? static_cast<uint32_t>(lane & 1)
+                                : h0 ^ static_cast<uint32_t>((wmn + i * C::kGroupWaves) & 1);
           const int tap = h ? tap_hi : tap_lo;
           const bool ok = t_ok && ((s_ok[i] >> tap) & 1u);
           a_off[i] = ok ? s_base[i] + static_cast<uint32_t>(h ? del_hi : del_lo) : kFar;
         }
       }
       return p;
-    };
-    // packed x: the bytes of this wave's A segments of the stage in flight,
-    // expanded to bf16 0/1 and written where the direct load would have
-    // put them, once the stage's MFMAs are issued
-    uint32_t pk[C::kAPer];
-    auto write_packed = [&](int buf) __attribute__((always_inline)) {
-      unsigned char* stage = smem + buf * C::kStageBytes;
-#pragma unroll
-      for (int i = 0; i < C::kAPer; ++i) {
-        const int q = wmn + i * C::kGroupWaves;
-        *reinterpret_cast<u32x4*>(stage + (kg * C::BM + kDmaRows * q) * kRowBytes + lane * 16) =
-            bits_to_bf16x8(pk[i]);
-      }
     };
     // enqueue the direct global->LDS load of segment i of a stage.  A ring
     // slot past the loop is loaded too (never read; its offsets stay inside
@@ -556,15 +556,17 @@ void conv3x3_kernel(ConvArgs a) {
     auto issue_seg = [&](const StageAddr& p, int i, int buf) {
       unsigned char* stage = smem + buf * C::kStageBytes;
       if (i < C::kAPer) {  // resolved at compile time
-        const int q = wmn + i * C::kGroupWaves;
         // (the offset goes through a variable: with the sum written in the
         // call, hipcc's host pass drops the kernel's launch stub)
         const uint32_t off = a_off[i] + p.da;
         if constexpr (PK) {
-          // packed x: the 8 spikes of this chunk are one byte at a sixteenth
-          // of the bf16 offset (past-the-end offsets stay past the end)
-          pk[i] = __builtin_amdgcn_raw_buffer_load_b8(xr, off >> 4, 0, 0);
+          // packed x: the 32 spikes of this lane's half-row are 4 bytes at a
+          // sixteenth of the bf16 offset (past-the-end offsets stay past it)
+          const int q = (wmn + i * C::kGroupWaves) % C::kSegA;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              xr, (lds_ptr_t)(stage + kg * C::BM * 8 + q * 256), 4, off >> 4, 0, 0, 0);
         } else {
+          const int q = wmn + i * C::kGroupWaves;
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               xr, (lds_ptr_t)(stage + (kg * C::BM + kDmaRows * q) * kRowBytes), 16, off, 0, 0, 0);
         }
@@ -573,7 +575,7 @@ void conv3x3_kernel(ConvArgs a) {
         const bool upper = (h0 ^ static_cast<uint32_t>(q & 1)) != 0;
         const uint32_t off = (p.zero_b || (p.tail && upper)) ? kFar : s_base[i] + p.db;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            wr, (lds_ptr_t)(stage + (KSPLIT * C::BM + kg * C::BN + kDmaRows * q) * kRowBytes),
+            wr, (lds_ptr_t)(stage + C::kAStageBytes + (kg * C::BN + kDmaRows * q) * kRowBytes),
             16, off, 0, 0, 0);
       }
     };
@@ -585,7 +587,6 @@ void conv3x3_kernel(ConvArgs a) {
       const StageAddr sp = prepare(p);
 #pragma unroll
       for (int i = 0; i < C::kSegPer; ++i) issue_seg(sp, i, p);
-      if constexpr (PK) write_packed(p);
     }
     // set-up that no load waits for
     if (tc == 0) {
@@ -618,13 +619,28 @@ void conv3x3_kernel(ConvArgs a) {
 
       const unsigned char* st = smem + buf * C::kStageBytes;
       const uint16_t* sa = reinterpret_cast<const uint16_t*>(st) + (kg * C::BM + wm * TM * 32 + r_lane) * kRow;
-      const uint16_t* sb = reinterpret_cast<const uint16_t*>(st) +
-                           (KSPLIT * C::BM + kg * C::BN + wn * TN * 32 + r_lane) * kRow;
+      const uint16_t* sb = reinterpret_cast<const uint16_t*>(st + C::kAStageBytes) +
+                           (kg * C::BN + wn * TN * 32 + r_lane) * kRow;
+      // packed A: the stage's 64 bits of each of this lane's rows; slice kk,
+      // half g reads byte 2*kk + g (K values 16*kk + 8*g ..)
+      u32x2 pa[TM];
+      if constexpr (PK) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          pa[i] = *reinterpret_cast<const u32x2*>(st + (kg * C::BM + wm * TM * 32 + i * 32 + r_lane) * 8);
+      }
       auto read = [&](bf16x8 (&fa)[TM], bf16x8 (&fb)[TN], int kk) {
         // tile rows start at multiples of 32, so the swizzle depends on r_lane only
         const int ch = swz(r_lane, kk * 2 + g_lane) * 8;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kRow + ch);
+        for (int i = 0; i < TM; ++i) {
+          if constexpr (PK) {
+            const u32x4 e = bits_to_bf16x8((pa[i][kk >> 1] >> (16 * (kk & 1) + 8 * g_lane)) & 0xFFu);
+            __builtin_memcpy(&fa[i], &e, 16);
+          } else {
+            fa[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kRow + ch);
+          }
+        }
 #pragma unroll
         for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRow + ch);
       };
@@ -646,7 +662,6 @@ void conv3x3_kernel(ConvArgs a) {
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
       }
-      if constexpr (PK) write_packed(nbuf);
       sp = prepare(s + C::kBuf);
       buf = buf + 1 == C::kBuf ? 0 : buf + 1;
     }
@@ -766,7 +781,7 @@ void conv3x3_kernel(ConvArgs a) {
 template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int MODE, int TAPS,
           bool PK>
 int launch_cfg(const ConvArgs& a, hipStream_t stream) {
-  using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF>;
+  using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF, PK>;
   const int64_t per_xcd = (static_cast<int64_t>(a.tiles_m) * a.tiles_n * a.splits + 7) / 8;
   if (per_xcd * 8 > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
   hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, NBUF, POOL, MODE, TAPS, PK>),
@@ -832,7 +847,8 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
 }
 
 // Packed-input LIF variants, instantiated in conv_packed.hip: the 3x3 conv
-// with or without the 2x2 pool (taps = 9) and the Linear (taps = 1).
+// with or without the 2x2 pool (taps = 9) and the Linear with or without
+// the OR of column groups of four (taps = 1).
 int dispatch_packed(const ConvArgs& a, const Plan& p, void* workspace, hipStream_t s, bool pool,
                     int taps);
 

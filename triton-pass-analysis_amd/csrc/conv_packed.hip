@@ -9,7 +9,10 @@ namespace snnk {
 
 int dispatch_packed(const ConvArgs& a, const Plan& p, void* workspace, hipStream_t s, bool pool,
                     int taps) {
-  if (taps == 1) return pool ? SNNK_EUNSUPPORTED : dispatch<false, MODE_LIF, 1, true>(a, p, workspace, s);
+  if (taps == 1) {  // with pool: the OR of each group of four adjacent columns
+    return pool ? dispatch<true, MODE_LIF, 1, true>(a, p, workspace, s)
+                : dispatch<false, MODE_LIF, 1, true>(a, p, workspace, s);
+  }
   if (pool) return dispatch<true, MODE_LIF, 9, true>(a, p, workspace, s);
   return dispatch<false, MODE_LIF, 9, true>(a, p, workspace, s);
 }

@@ -119,6 +119,7 @@ PROTOTYPES: dict[str, list] = {
         _p, _i32, _p, _p,      # x, x_fmt, w, bias
         _p, _i32,              # spikes_out, out_fmt
         _i64, _i64, _i64, _i64,  # T, R, K, N
+        _i32,                  # col_pool
         _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
         _i32, _i32,            # soft_reset, tile_hint
         _i32, _p, _i64,        # splits, workspace, workspace_bytes
@@ -163,6 +164,13 @@ PROTOTYPES: dict[str, list] = {
         _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
         _i32, _p,              # soft_reset, stream
     ],
+    "snnk_conv3x3_image_lif_act": [
+        _p, _p, _p, _p, _i32,  # image, w, bias, spikes_out, out_fmt
+        _i64, _i64, _i64,      # T, B, Cin
+        _i64, _i64, _i64,      # H, W, Cout
+        _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
+        _i32, _p,              # soft_reset, stream
+    ],
     "snnk_to_nhwc_bf16": [
         _p, _i32, _p,          # src, src_dtype, dst
         _i64, _i64, _i64,      # N, C, HW
@@ -176,6 +184,10 @@ SIZE_PROTOTYPES: dict[str, list] = {
                                     _i32, _i32, _i32, _i32],           # pool, preact, tile, splits
     "snnk_linear_bias_lif_ws_size": [_i64, _i64, _i64, _i64,            # T, R, K, N
                                      _i32, _i32, _i32],                 # preact, tile, splits
+    "snnk_conv3x3_bn_lif_act_ws_size": [_i64, _i64, _i64, _i64, _i64, _i64,  # T, B, H, W, Cin, Cout
+                                        _i32, _i32, _i32, _i32],        # pool, x_fmt, tile, splits
+    "snnk_linear_bias_lif_act_ws_size": [_i64, _i64, _i64, _i64,        # T, R, K, N
+                                         _i32, _i32, _i32, _i32],       # x_fmt, col_pool, tile, splits
 }
 
 _lib = None

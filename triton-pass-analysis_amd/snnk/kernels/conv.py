@@ -155,8 +155,8 @@ def conv3x3_bn_lif_act(x: torch.Tensor, w_prep: torch.Tensor, bias: torch.Tensor
         assert out.shape == shape and out.dtype == dt and out.is_contiguous()
     sp = 0 if splits is None else int(splits)
     with torch.cuda.device(x.device):
-        nbytes = _abi.size_call("snnk_conv3x3_bn_lif_ws_size", T, B, H, W, Cin, Cout,
-                                1 if pool else 0, 0, int(tile_hint), sp)
+        nbytes = _abi.size_call("snnk_conv3x3_bn_lif_act_ws_size", T, B, H, W, Cin, Cout,
+                                1 if pool else 0, x_fmt, int(tile_hint), sp)
         ws = _workspace.get(x.device, nbytes)
         _abi.call("snnk_conv3x3_bn_lif_act", x.data_ptr(), x_fmt, w_prep.data_ptr(),
                   _abi.ptr(bias), out.data_ptr(), _abi.ACT_BITS if out_bits else _abi.ACT_BF16,
@@ -181,8 +181,9 @@ def conv3x3_preact_nhwc(x: torch.Tensor, w_prep: torch.Tensor, bias: torch.Tenso
 def conv3x3_image_lif(image: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
                       T: int, *, decay: float, in_scale: float, v_threshold: float,
                       v_reset: float = 0.0, soft_reset: bool = False,
-                      out: torch.Tensor | None = None) -> torch.Tensor:
-    """Static image [B, Cin, H, W] fp32 shown at T steps -> NHWC bf16 spikes [T, B, H, W, Cout]."""
+                      out: torch.Tensor | None = None, out_bits: bool = False) -> torch.Tensor:
+    """Static image [B, Cin, H, W] fp32 shown at T steps -> NHWC bf16 spikes
+    [T, B, H, W, Cout], or with ``out_bits`` int32 packed words [T, B, H, W, Cout // 32]."""
     assert image.is_cuda and image.dtype == torch.float32 and image.ndim == 4
     image = image.contiguous()
     B, Cin, H, W = image.shape
@@ -192,12 +193,14 @@ def conv3x3_image_lif(image: torch.Tensor, weight: torch.Tensor, bias: torch.Ten
     if bias is not None:
         bias = bias.float().contiguous()
     if out is None:
-        out = torch.empty(T, B, H, W, Cout, device=image.device, dtype=torch.bfloat16)
+        out = (torch.empty(T, B, H, W, Cout // 32, device=image.device, dtype=torch.int32)
+               if out_bits else
+               torch.empty(T, B, H, W, Cout, device=image.device, dtype=torch.bfloat16))
     with torch.cuda.device(image.device):
-        _abi.call("snnk_conv3x3_image_lif", image.data_ptr(), w.data_ptr(), _abi.ptr(bias),
-                  out.data_ptr(), T, B, Cin, H, W, Cout, float(decay), float(in_scale),
-                  float(v_threshold), float(v_reset), 1 if soft_reset else 0,
-                  _abi.stream(image.device))
+        _abi.call("snnk_conv3x3_image_lif_act", image.data_ptr(), w.data_ptr(), _abi.ptr(bias),
+                  out.data_ptr(), _abi.ACT_BITS if out_bits else _abi.ACT_BF16, T, B, Cin, H,
+                  W, Cout, float(decay), float(in_scale), float(v_threshold), float(v_reset),
+                  1 if soft_reset else 0, _abi.stream(image.device))
     return out
 
 

@@ -69,26 +69,29 @@ def _linear_call(x, w, bias, out, pre, decay, in_scale, v_threshold, v_reset, so
 def linear_bias_lif_act(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
                         decay: float, in_scale: float, v_threshold: float,
                         v_reset: float = 0.0, soft_reset: bool = False, out_bits: bool = True,
-                        out: torch.Tensor | None = None, tile_hint: int = -1,
-                        splits: int | None = None) -> torch.Tensor:
+                        col_pool: bool = False, out: torch.Tensor | None = None,
+                        tile_hint: int = -1, splits: int | None = None) -> torch.Tensor:
     """:func:`linear_bias_lif` with bit-packed activations on either side.
 
     x: bf16 0/1 ``[T, R, K]`` or int32 packed words ``[T, R, K // 32]``;
     returns int32 words ``[T, R, N // 32]`` (``out_bits=True``) or bf16
-    ``[T, R, N]``, the same spikes as the bf16 path."""
+    ``[T, R, N]``, the same spikes as the bf16 path.  ``col_pool``: the OR of
+    each group of four adjacent output columns (bf16 ``[T, R, N // 4]``, as
+    :func:`linear_bias_lif_pool4`)."""
     assert x.is_cuda and x.ndim == 3 and x.is_contiguous()
     if x.dtype == torch.int32:
         x_fmt, K = _abi.ACT_BITS, x.shape[2] * 32
     else:
         assert x.dtype == torch.bfloat16, x.dtype
         x_fmt, K = _abi.ACT_BF16, x.shape[2]
+    assert not (col_pool and out_bits), "the column-pooled output is bf16"
     T, R = x.shape[:2]
     N = w.shape[0]
     assert w.dtype == torch.bfloat16 and w.shape == (N, K) and w.is_contiguous() \
         and w.device == x.device
     if bias is not None:
         assert bias.dtype == torch.float32 and bias.numel() == N and bias.is_contiguous()
-    shape = (T, R, N // 32 if out_bits else N)
+    shape = (T, R, N // 4 if col_pool else (N // 32 if out_bits else N))
     dt = torch.int32 if out_bits else torch.bfloat16
     if out is None:
         out = torch.empty(shape, device=x.device, dtype=dt)
@@ -96,12 +99,13 @@ def linear_bias_lif_act(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | N
         assert out.shape == shape and out.dtype == dt and out.is_contiguous()
     sp = 0 if splits is None else int(splits)
     with torch.cuda.device(x.device):
-        nbytes = _abi.size_call("snnk_linear_bias_lif_ws_size", T, R, K, N, 0, int(tile_hint), sp)
+        nbytes = _abi.size_call("snnk_linear_bias_lif_act_ws_size", T, R, K, N, x_fmt,
+                                1 if col_pool else 0, int(tile_hint), sp)
         ws = _workspace.get(x.device, nbytes)
         _abi.call("snnk_linear_bias_lif_act", x.data_ptr(), x_fmt, w.data_ptr(), _abi.ptr(bias),
                   out.data_ptr(), _abi.ACT_BITS if out_bits else _abi.ACT_BF16, T, R, K, N,
-                  float(decay), float(in_scale), float(v_threshold), float(v_reset),
-                  1 if soft_reset else 0, int(tile_hint), sp, _abi.ptr(ws),
+                  1 if col_pool else 0, float(decay), float(in_scale), float(v_threshold),
+                  float(v_reset), 1 if soft_reset else 0, int(tile_hint), sp, _abi.ptr(ws),
                   0 if ws is None else ws.numel(), _abi.stream(x.device))
     return out
 

@@ -16,9 +16,12 @@ from ..kernels.fused import (
     fused_bias_if_lif, fused_bias_if_lif_rate, fused_bias_if_lif_stateful, fold_conv_bn,
 )
 from ..kernels.conv import (
-    prepare_conv3x3_weight, to_nhwc_bf16, conv3x3_bn_lif_nhwc, conv3x3_dense_weight,
+    prepare_conv3x3_weight, to_nhwc_bf16, conv3x3_bn_lif_nhwc, conv3x3_bn_lif_act,
+    conv3x3_dense_weight,
 )
-from ..kernels.linear import linear_bias_lif, linear_bias_lif_pool4, linear_fusable
+from ..kernels.linear import (
+    linear_bias_lif, linear_bias_lif_act, linear_bias_lif_pool4, linear_fusable,
+)
 
 
 def _thr(module, v_threshold):
@@ -336,8 +339,13 @@ class FusedConvBNLIFPool(nn.Module):
             cache[(H, W)] = hit
         return hit[1]
 
-    def forward_nhwc(self, x_nhwc, out=None, tile_hint=-1):
-        T, B, H, W, C = x_nhwc.shape
+    def forward_nhwc(self, x_nhwc, out=None, tile_hint=-1, out_bits=False):
+        """Spikes in, spikes out, channels last: ``x_nhwc`` is bf16 0/1
+        ``[T, B, H, W, C]`` or int32 packed words ``[T, B, H, W, C // 32]``
+        (bit c%32 of word c//32).  ``out_bits`` asks for packed words out; the
+        2x2-map layer with pooling (column-pooled dense form) writes bf16."""
+        packed = x_nhwc.dtype == torch.int32
+        T, B, H, W = x_nhwc.shape[:4]
         lif = dict(decay=self.decay_factor, in_scale=self.input_scale,
                    v_threshold=self.v_threshold, v_reset=self.v_reset,
                    soft_reset=self.soft_reset)
@@ -346,15 +354,23 @@ class FusedConvBNLIFPool(nn.Module):
             # every output pixel sees the whole map: one dense Linear + LIF
             # (+ the pool as an OR of column groups), no padding taps
             w_d, b_d = self._dense(H, W)
-            x2 = x_nhwc.reshape(T, B, H * W * C)
+            x2 = x_nhwc.reshape(T, B, -1)
             Cout = self.weight.shape[0]
             if self.pool == "max":
                 o2 = None if out is None else out.view(T, B, Cout)
-                y = linear_bias_lif_pool4(x2, w_d, b_d, out=o2, **lif)
+                y = (linear_bias_lif_act(x2, w_d, b_d, out_bits=False, col_pool=True, out=o2, **lif)
+                     if packed else linear_bias_lif_pool4(x2, w_d, b_d, out=o2, **lif))
                 return y.view(T, B, 1, 1, Cout)
+            if packed or out_bits:
+                o2 = None if out is None else out.view(T, B, -1)
+                y = linear_bias_lif_act(x2, w_d, b_d, out_bits=out_bits, out=o2, **lif)
+                return y.view(T, B, H, W, -1)
             o2 = None if out is None else out.view(T, B, H * W * Cout)
             y = linear_bias_lif(x2, w_d, b_d, out=o2, **lif)
             return y.view(T, B, H, W, Cout)
+        if packed or out_bits:
+            return conv3x3_bn_lif_act(x_nhwc, self.w_prep, self.bias, pool=self.pool == "max",
+                                      out_bits=out_bits, out=out, tile_hint=tile_hint, **lif)
         return conv3x3_bn_lif_nhwc(x_nhwc, self.w_prep, self.bias, pool=self.pool == "max",
                                    out=out, tile_hint=tile_hint, **lif)
 

@@ -30,7 +30,7 @@ from ..nn.modules import (
 from ..passes.fuse import fuse_snn_model
 from ..kernels.conv import conv3x3_image_lif
 from ..kernels.fused import fold_conv_bn
-from ..kernels.linear import linear_bias_lif, linear_preact, linear_mean_t
+from ..kernels.linear import linear_bias_lif, linear_bias_lif_act, linear_preact, linear_mean_t
 from ..kernels.neurons import neuron_params
 
 VGG16_CFG = [64, 64, "P", 128, 128, "P", 256, 256, 256, "P",
@@ -48,6 +48,19 @@ def _neuron_factory(neuron, *, tau, decay_input, soft_reset, v_threshold, v_rese
     return LIFNode(tau=tau, decay_input=decay_input, soft_reset=soft_reset,
                    v_threshold=v_threshold, v_reset=v_reset, layout=layout)
 
+
+_POPCOUNT8 = None
+
+
+def spike_rate(s: torch.Tensor) -> torch.Tensor:
+    """Mean firing rate of bf16 0/1 spikes or of int32 packed words (popcount)."""
+    global _POPCOUNT8
+    if s.dtype != torch.int32:
+        return s.float().mean()
+    if _POPCOUNT8 is None or _POPCOUNT8.device != s.device:
+        _POPCOUNT8 = torch.tensor([bin(i).count("1") for i in range(256)], dtype=torch.float32,
+                                  device=s.device)
+    return _POPCOUNT8[s.contiguous().view(torch.uint8).long()].sum() / (s.numel() * 32)
 
 class VGGSNN(nn.Module):
     """forward(x_seq [T, B, 3, H, W]) -> [T, B, num_classes]
@@ -237,6 +250,9 @@ class FusedVGGSNN(nn.Module):
         self.register_buffer("fc3_w", w3.to(torch.bfloat16).contiguous())
         self.register_buffer("fc3_b", b3.contiguous())
         self.num_classes = n_cls
+        # spikes between conv layers as packed words (SNNK_ACT_BITS): the conv
+        # kernels read and write them directly (set False for bf16 0/1)
+        self.bits_between_layers = True
         self._graphs = {}
 
     def _lif(self):
@@ -244,18 +260,24 @@ class FusedVGGSNN(nn.Module):
                     v_reset=self.v_reset, soft_reset=self.soft)
 
     def features_nhwc(self, image: torch.Tensor, rates: list | None = None) -> torch.Tensor:
-        """image [B, 3, H, W] fp32 -> NHWC bf16 spikes of the last conv block.
-        ``rates`` (optional list) receives every layer's mean firing rate."""
-        x = conv3x3_image_lif(image, self.w0, self.b0, self.T, **self._lif())
+        """image [B, 3, H, W] fp32 -> spikes of the last conv block, channels
+        last: bf16 ``[T, B, H, W, C]`` or (``bits_between_layers``) int32 packed
+        words ``[T, B, H, W, C // 32]``.  Between conv layers the spikes travel
+        as packed words (16x fewer bytes than bf16) when ``bits_between_layers``
+        is set.  ``rates`` (optional list) receives every layer's mean firing rate."""
+        # packed from the first layer on, unless a pool follows it directly
+        x = conv3x3_image_lif(image, self.w0, self.b0, self.T, **self._lif(),
+                              out_bits=self.bits_between_layers and not self.pool0
+                              and self.w0.shape[0] % 32 == 0)
         if rates is not None:
-            rates.append(x.float().mean())
+            rates.append(spike_rate(x))
         if self.pool0:
             T, B, H, W, C = x.shape
             x = x.view(T, B, H // 2, 2, W // 2, 2, C).amax(dim=(3, 5)).contiguous()
         for conv in self.convs:
-            x = conv.forward_nhwc(x)
+            x = conv.forward_nhwc(x, out_bits=self.bits_between_layers)
             if rates is not None:
-                rates.append(x.float().mean())
+                rates.append(spike_rate(x))
         return x
 
     def forward(self, image: torch.Tensor, rates: list | None = None,
@@ -278,7 +300,9 @@ class FusedVGGSNN(nn.Module):
         R = (B + 3) // 4 * 4
         if R != B:
             x = F.pad(x, (0, 0, 0, R - B))
-        x = linear_bias_lif(x, self.fc1_w, self.fc1_b, **self._lif())
+        # FC1 takes the features in whichever format the last conv wrote
+        x = (linear_bias_lif_act(x, self.fc1_w, self.fc1_b, out_bits=False, **self._lif())
+             if x.dtype == torch.int32 else linear_bias_lif(x, self.fc1_w, self.fc1_b, **self._lif()))
         if rates is not None:
             rates.append(x[:, :B].float().mean())
         x = linear_bias_lif(x, self.fc2_w, self.fc2_b, **self._lif())
