@@ -83,6 +83,31 @@ def cpu_threads() -> int:
     return n
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name"; /proc/cpuinfo's
+    "model name" when lscpu is absent)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(value: float, unit: str, sample: str, seconds: float, kind: str = "port"):
+    return {"value": value, "unit": unit, "cores": torch.get_num_threads(), "kind": kind,
+            "cpu_model": cpu_model(), "sample": sample, "seconds_per_call": seconds}
+
+
 def time_cpu(fn, budget_s: float = 8.0, min_runs: int = 3) -> float:
     """Median seconds of fn() after one warm-up run, within a time budget."""
     fn()
@@ -185,6 +210,15 @@ def bench_lif(args, dev):
     want = ob.pack_rows(s_ref.reshape(T, -1, 32).numpy()).reshape(T, -1)
     ok_bits = bool(np.array_equal(ws[0].cpu().numpy().view(np.uint32), want))
 
+    # measured ceiling: a plain device copy moving the same bytes (half read,
+    # half written), timed the same way over the same number of rotating sets
+    n_copy = bytes_per // 8
+    csrc = [torch.rand(n_copy, device=dev) for _ in range(nsets)]
+    cdst = [torch.empty_like(csrc[0]) for _ in range(nsets)]
+    _, copy_ms = time_gpu(lambda i: cdst[i].copy_(csrc[i]), nsets, args.steps, args.warmup)
+    copy_gbs = 2 * n_copy * 4 / (copy_ms * 1e-3) / 1e9
+    del csrc, cdst
+
     rec = {
         "workload": "lif", "value": bytes_per / wall / 1e9, "unit": "GB/s",
         "ms_per_step": wall * 1e3, "dtype": "f32",
@@ -197,7 +231,13 @@ def bench_lif(args, dev):
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": bytes_per / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                      "traffic": None, "algorithmic_bytes": bytes_per,
-                     "kernel_ms_mean": kern_ms},
+                     "kernel_ms_mean": kern_ms,
+                     "ceiling_measured": {
+                         "kernel": "torch copy_ of %d fp32 (same bytes: %.1f MB read + %.1f MB "
+                                   "written)" % (n_copy, n_copy * 4e-6, n_copy * 4e-6),
+                         "achieved": copy_gbs, "unit": "GB/s", "kernel_ms_mean": copy_ms,
+                         "frac_of_peak": copy_gbs / HBM_PEAK_GBS,
+                         "lif_frac_of_ceiling": bytes_per / (kern_ms * 1e-3) / 1e9 / copy_gbs}},
         "parity": ok and ok_bits,
         "spikes_packed": {"value": bits_bytes / wall_b / 1e9, "unit": "GB/s",
                           "algorithmic_bytes": bits_bytes, "kernel_ms_mean": kern_b,
@@ -211,11 +251,10 @@ def bench_lif(args, dev):
         nth = cpu_threads()
         torch.set_num_threads(nth)
         sec = time_cpu(lambda: on.lif_multistep(x_cpu, neuron="lif", tau=2.0))
-        rec["cpu_baseline"] = {"value": bytes_per / sec / 1e9, "unit": "GB/s",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": "oracle.neurons.lif_multistep (torch CPU restatement "
-                                         "of naive_if_lif + final v) on the full LIF config",
-                               "seconds_per_call": sec}
+        rec["cpu_baseline"] = cpu_baseline(
+            bytes_per / sec / 1e9, "GB/s",
+            "oracle.neurons.lif_multistep (torch CPU restatement of naive_if_lif + final v) "
+            "on the full LIF config", sec)
     return rec
 
 
@@ -319,11 +358,10 @@ def bench_bgemm(args, dev):
         Af, Wf = A.float(), W.float()
         rows = 2048
         sec = time_cpu(lambda: Af[:rows] @ Wf, budget_s=6.0)
-        rec["cpu_baseline"] = {"value": 2.0 * rows * N * K / sec / 1e12, "unit": "TOPS",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": f"exact fp32 matmul of the {{0,1}} operands "
-                                         f"(counts < 2^24), first {rows} of {M} rows",
-                               "seconds_per_call": sec}
+        rec["cpu_baseline"] = cpu_baseline(
+            2.0 * rows * N * K / sec / 1e12, "TOPS",
+            f"exact fp32 matmul of the {{0,1}} operands (counts < 2^24), first {rows} of "
+            f"{M} rows", sec)
     return rec
 
 
@@ -343,9 +381,15 @@ def _conv_block_params(g, Cin, Cout):
 
 
 def bench_conv(args, dev):
+    """The fused block as the VGG engine runs it: spikes in and out as packed
+    words (bit c%32 of word c/32 per pixel), so the block reads 0.52 MB of
+    input spikes and writes 0.26 MB of output spikes; the bf16 0/1 variant
+    (16.8 MB in, 4.19 MB out) is timed beside it."""
+    import numpy as np
     from snnk.kernels import conv as kc
+    from snnk.kernels.binary import pack_bits
     from snnk.kernels.fused import fold_conv_bn
-    from oracle import fused as of
+    from oracle import bits as ob, fused as of
 
     T, B, Cin, Cout, H, W = 4, 32, 128, 256, 16, 16
     g = torch.Generator().manual_seed(0)
@@ -355,20 +399,39 @@ def bench_conv(args, dev):
     wp = kc.prepare_conv3x3_weight(w2.to(dev))
     bd = b2.to(dev).float().contiguous()
     xd = kc.to_nhwc_bf16(x.to(dev))
+    xw = pack_bits(xd, dim=-1)
+    Ho, Wo = H // 2, W // 2
     flops = 2.0 * T * B * H * W * Cout * Cin * 9
-    set_bytes = xd.numel() * 2 + T * B * (H // 2) * (W // 2) * Cout * 2
-    nsets = max(2, math.ceil(ROTATE_BYTES / set_bytes))
-    xs = [xd.clone() for _ in range(nsets)]
-    outs = [torch.empty(T, B, H // 2, W // 2, Cout, device=dev, dtype=torch.bfloat16)
-            for _ in range(nsets)]
+    w_bytes = wp.numel() * 2 + bd.numel() * 4
+    in_bits, out_bits = xw.numel() * 4, T * B * Ho * Wo * Cout // 8
+    in_bf16, out_bf16 = xd.numel() * 2, T * B * Ho * Wo * Cout * 2
+    nsets = max(2, math.ceil(ROTATE_BYTES / (in_bf16 + out_bf16)))
+    xws = [xw.clone() for _ in range(nsets)]
+    xds = [xd.clone() for _ in range(nsets)]
+    ows = [torch.empty(T, B, Ho, Wo, Cout // 32, device=dev, dtype=torch.int32)
+           for _ in range(nsets)]
+    obs = [torch.empty(T, B, Ho, Wo, Cout, device=dev, dtype=torch.bfloat16)
+           for _ in range(nsets)]
+    lif = dict(pool=True, decay=0.5, in_scale=0.5, v_threshold=1.0)
 
     def step(i):
-        kc.conv3x3_bn_lif_nhwc(xs[i], wp, bd, pool=True, decay=0.5, in_scale=0.5,
-                               v_threshold=1.0, out=outs[i])
+        kc.conv3x3_bn_lif_act(xws[i], wp, bd, out=ows[i], **lif)
+
+    def step_bf16(i):
+        kc.conv3x3_bn_lif_nhwc(xds[i], wp, bd, out=obs[i], **lif)
 
     wall, kern_ms = time_gpu(step, nsets, args.steps, args.warmup)
+    wall_bf, kern_bf = time_gpu(step_bf16, nsets, args.steps, args.warmup)
     ref, _ = of.conv_bn_lif_pool(x, w, None, gamma, beta, mean, var, 1e-5, pool=True)
-    agree = (outs[0].float().cpu().permute(0, 1, 4, 2, 3) == ref).float().mean().item()
+    ref_nhwc = ref.permute(0, 1, 3, 4, 2).contiguous()
+    # packed words vs the oracle's spikes packed the reference's way (LSB first)
+    want = ob.pack_rows(ref_nhwc.reshape(-1, Cout).numpy().astype(np.uint8))
+    got = ows[0].cpu().numpy().view(np.uint32).reshape(-1, Cout // 32)
+    flips = int(np.unpackbits((got ^ want).view(np.uint8)).sum())
+    agree = 1.0 - flips / ref.numel()
+    agree_bf = (obs[0].float().cpu() == ref_nhwc).float().mean().item()
+    # the two formats carry the same spikes
+    same = bool(torch.equal(pack_bits(obs[0], dim=-1), ows[0]))
     # NCHW fp32 -> NHWC bf16 conversion at the block boundary (outside the step)
     x_nchw = x.to(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -378,60 +441,88 @@ def bench_conv(args, dev):
     e1.record()
     torch.cuda.synchronize()
     achieved = flops / (kern_ms * 1e-3) / 1e12
+    ach_bf = flops / (kern_bf * 1e-3) / 1e12
     rec = {
         "workload": "conv", "value": flops / wall / 1e12, "unit": "TFLOP/s",
-        "ms_per_step": wall * 1e3, "dtype": "bf16 x bf16 -> f32 acc, f32 LIF",
+        "ms_per_step": wall * 1e3, "dtype": "bf16 x bf16 -> f32 acc, f32 LIF; u1 spikes",
         "config": {"workload": "conv3x3_bn_lif_maxpool_T4_B32_C128to256_16x16", "T": T, "B": B,
                    "Cin": Cin, "Cout": Cout, "H": H, "W": W, "input_p": 0.15,
-                   "layout": "NHWC bf16 in/out", "rotating_sets": nsets},
-        "roofline": {"bound": "mfma", "kernel": "conv3x3_kernel",
+                   "layout": "NHWC; spikes in and out as packed u32 words along C (LSB first)",
+                   "rotating_sets": nsets},
+        "roofline": {"bound": "mfma", "kernel": "conv3x3_kernel (packed A)",
                      "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
                      "algorithmic_flops": flops, "kernel_ms_mean": kern_ms},
+        "bytes": {"spikes_in": in_bits, "spikes_out": out_bits, "weights_bias": w_bytes,
+                  "bf16_spikes_in": in_bf16, "bf16_spikes_out": out_bf16},
+        "variants": {"bf16_spikes": {"kernel_ms_mean": kern_bf, "achieved": ach_bf,
+                                     "unit": "TFLOP/s", "frac": ach_bf / BF16_PEAK_TFLOPS,
+                                     "ms_per_step": wall_bf * 1e3,
+                                     "spike_agreement_vs_fp32": agree_bf}},
         "spike_agreement_vs_fp32": agree,
+        "packed_equals_bf16_path": same,
         "nchw_to_nhwc_ms": e0.elapsed_time(e1) / 20,
-        "parity": agree >= 0.999,
+        "parity": agree >= 0.999 and agree_bf >= 0.999 and same,
     }
     _with_traffic(rec["roofline"], "conv")
     if not args.no_cpu_baseline:
         torch.set_num_threads(cpu_threads())
         sec = time_cpu(lambda: of.conv_bn_lif_pool(x, w, None, gamma, beta, mean, var, 1e-5,
                                                    pool=True), budget_s=6.0)
-        rec["cpu_baseline"] = {"value": flops / sec / 1e12, "unit": "TFLOP/s",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": "oracle.fused.conv_bn_lif_pool (fold_conv_bn + "
-                                         "F.conv2d fp32 + LIF + max_pool2d) on the full config",
-                               "seconds_per_call": sec}
+        rec["cpu_baseline"] = cpu_baseline(
+            flops / sec / 1e12, "TFLOP/s",
+            "oracle.fused.conv_bn_lif_pool (fold_conv_bn + F.conv2d fp32 + LIF + max_pool2d) "
+            "on the full config", sec)
     return rec
 
 
 # --------------------------------------------------------------------------
 # VGG16-SNN end to end (the headline)
 # --------------------------------------------------------------------------
+def _unpack_words(words: torch.Tensor, C: int) -> torch.Tensor:
+    """int32 words [..., C/32] (bit c%32 of word c/32) -> fp32 0/1 [..., C]."""
+    bits = (words.unsqueeze(-1) >> torch.arange(32, device=words.device)) & 1
+    return bits.reshape(*words.shape[:-1], C).float()
+
+
+def _image_out_bits(eng) -> bool:
+    return eng.bits_between_layers and not eng.pool0 and eng.w0.shape[0] % 32 == 0
+
+
 def _vgg_layer_steps(eng, image, T):
-    """(name, flops, step(out_idx)) for every kernel of one forward, each fed
-    the activations the engine itself produced."""
+    """(name, flops, step()) for every kernel of one forward, each fed the
+    activations the engine itself produced, in the engine's formats (packed
+    words between conv layers, bf16 out of the pooled 2x2 layer)."""
     from snnk.kernels.conv import conv3x3_image_lif
-    from snnk.kernels.linear import linear_bias_lif, linear_mean_t
+    from snnk.kernels.linear import linear_bias_lif, linear_bias_lif_act, linear_mean_t
 
     B = image.shape[0]
     lif = eng._lif()
+    bits = eng.bits_between_layers
     steps = []
-    x = conv3x3_image_lif(image, eng.w0, eng.b0, T, **lif)
-    H, W, C0 = x.shape[2], x.shape[3], x.shape[4]
+    ob0 = _image_out_bits(eng)
+    x = conv3x3_image_lif(image, eng.w0, eng.b0, T, out_bits=ob0, **lif)
+    H, W, C0 = x.shape[2], x.shape[3], eng.w0.shape[0]
     o0 = torch.empty_like(x)
     steps.append(("L1 image 3->%d %dx%d" % (C0, H, W), 2.0 * B * H * W * C0 * 27,
-                  lambda: conv3x3_image_lif(image, eng.w0, eng.b0, T, out=o0, **lif)))
+                  lambda: conv3x3_image_lif(image, eng.w0, eng.b0, T, out=o0, out_bits=ob0,
+                                            **lif)))
+    assert not eng.pool0, "the VGG16 engine has no pool after its first layer"
+    Cin = C0
     for li, conv in enumerate(eng.convs):
         xin = x
-        x = conv.forward_nhwc(xin)
-        _, _, H, W, Cin = xin.shape
-        Cout = x.shape[-1]
+        x = conv.forward_nhwc(xin, out_bits=bits)
+        H, W = xin.shape[2], xin.shape[3]
+        Cout = conv.weight.shape[0]
         out = torch.empty_like(x)
         flops = 2.0 * T * B * H * W * Cout * Cin * 9
-        name = "L%d conv %d->%d %dx%d%s" % (li + 2, Cin, Cout, H, W,
-                                           " +pool" if conv.pool else "")
-        steps.append((name, flops, (lambda c=conv, a=xin, o=out: c.forward_nhwc(a, out=o))))
+        fmt = ("u1" if xin.dtype == torch.int32 else "bf16") + "->" + \
+              ("u1" if x.dtype == torch.int32 else "bf16")
+        name = "L%d conv %d->%d %dx%d%s %s" % (li + 2, Cin, Cout, H, W,
+                                              " +pool" if conv.pool else "", fmt)
+        steps.append((name, flops, (lambda c=conv, a=xin, o=out:
+                                    c.forward_nhwc(a, out=o, out_bits=bits))))
+        Cin = Cout
     R = (B + 3) // 4 * 4
     f = x.reshape(T, B, -1)
     if R != B:
@@ -441,16 +532,73 @@ def _vgg_layer_steps(eng, image, T):
                            ("FC2", eng.fc2_w, eng.fc2_b, False),
                            ("FC3", eng.fc3_w, eng.fc3_b, True)):
         fin = f
-        f = (linear_mean_t(fin, w, b) if last else linear_bias_lif(fin, w, b, **lif))
-        out = torch.empty_like(f)
+        if last:
+            f = linear_mean_t(fin, w, b)
+            fn = (lambda a=fin, w=w, b=b, o=torch.empty_like(f): linear_mean_t(a, w, b, out=o))
+        elif fin.dtype == torch.int32:
+            f = linear_bias_lif_act(fin, w, b, out_bits=False, **lif)
+            fn = (lambda a=fin, w=w, b=b, o=torch.empty_like(f):
+                  linear_bias_lif_act(a, w, b, out_bits=False, out=o, **lif))
+        else:
+            f = linear_bias_lif(fin, w, b, **lif)
+            fn = (lambda a=fin, w=w, b=b, o=torch.empty_like(f):
+                  linear_bias_lif(a, w, b, out=o, **lif))
         flops = 2.0 * T * B * w.shape[0] * w.shape[1]
         name = "%s %d->%d%s" % (nm, w.shape[1], w.shape[0], " +mean over T" if last else "")
-        if last:
-            steps.append((name, flops, (lambda a=fin, w=w, b=b, o=out: linear_mean_t(a, w, b, out=o))))
-        else:
-            steps.append((name, flops, (lambda a=fin, w=w, b=b, o=out:
-                                        linear_bias_lif(a, w, b, out=o, **lif))))
+        steps.append((name, flops, fn))
     return steps
+
+
+def _vgg_teacher_forced(eng, params, img_cpu, T, dev):
+    """Per-layer spike agreement of the engine with the fp32 oracle, every
+    layer fed the oracle's own input in the format the engine hands that layer
+    (packed words into the conv layers); FC3: max |logit error|."""
+    from snnk.kernels.binary import pack_bits
+    from snnk.kernels.conv import conv3x3_image_lif, to_nhwc_bf16
+    from snnk.kernels.linear import linear_bias_lif, linear_preact
+    from oracle import vgg as ov
+
+    B = img_cpu.shape[0]
+    rec = ov.forward_layers(params, img_cpu, T)
+    lif = eng._lif()
+    convs = iter(eng.convs)
+    fcs = [(eng.fc1_w, eng.fc1_b), (eng.fc2_w, eng.fc2_b)]
+    R = (B + 3) // 4 * 4
+    out = []
+    for r in rec:
+        if r["kind"] == "image":
+            y = conv3x3_image_lif(img_cpu.to(dev), eng.w0, eng.b0, T,
+                                  out_bits=_image_out_bits(eng), **lif)
+            C = eng.w0.shape[0]
+            name = "L1"
+        elif r["kind"] == "conv":
+            conv = next(convs)
+            x = to_nhwc_bf16(r["input"].to(dev))
+            if eng.bits_between_layers:
+                x = pack_bits(x, dim=-1)
+            y = conv.forward_nhwc(x, out_bits=eng.bits_between_layers)
+            C = conv.weight.shape[0]
+            name = "L%d" % (len(out) + 1)
+        elif r["kind"] == "fc_lif":
+            w, b = fcs.pop(0)
+            xp = torch.nn.functional.pad(r["input"], (0, 0, 0, R - B))
+            y = linear_bias_lif(xp.to(dev, torch.bfloat16).contiguous(), w, b, **lif)[:, :B]
+            out.append({"layer": "FC%d" % (3 - len(fcs) - 1),
+                        "agreement": (y.cpu().float() == r["output"]).float().mean().item(),
+                        "rate": r["output"].mean().item()})
+            continue
+        else:
+            xp = torch.nn.functional.pad(r["input"], (0, 0, 0, R - B))
+            y = linear_preact(xp.to(dev, torch.bfloat16).contiguous(), eng.fc3_w, eng.fc3_b)
+            err = (y.cpu()[:, :B, :eng.num_classes] - r["output"]).abs().max().item()
+            out.append({"layer": "FC3", "max_abs_logit_err": err,
+                        "logit_scale": r["output"].abs().max().item()})
+            continue
+        got = _unpack_words(y, C) if y.dtype == torch.int32 else y.float()
+        got = got.cpu().permute(0, 1, 4, 2, 3)
+        out.append({"layer": name, "agreement": (got == r["output"]).float().mean().item(),
+                    "rate": r["output"].mean().item()})
+    return out
 
 
 def bench_vgg(args, dev):
@@ -486,12 +634,16 @@ def bench_vgg(args, dev):
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) / args.steps
         gpu_ms = e0.elapsed_time(e1) / args.steps
+        # BASELINE's init leaves the deep layers silent, so this end-to-end
+        # check compares little more than the FC3 bias; the gain-3 per-layer
+        # figure below is the discriminating one
         logits = eng.run_graph(imgs[0], mean_t=True).cpu()
         ref = ov.forward(params, img_cpu, T).mean(0)
         ok = bool(torch.equal(logits.argmax(-1), ref.argmax(-1))) and \
             ((logits - ref).abs().max() / ref.abs().max()).item() < 1e-3
         recs[B] = dict(B=B, img_s=B / wall, ms=wall * 1e3, gpu_ms=gpu_ms, parity=ok,
                        img_cpu=img_cpu)
+        del graphs
     # per-layer kernels at B=32, each replayed alone in a graph
     B = 32
     image = recs[32]["img_cpu"].to(dev)
@@ -504,14 +656,28 @@ def bench_vgg(args, dev):
     dom = max(layers, key=lambda r: r["kernel_ms"])
     flops_fwd = sum(r["gflop"] for r in layers) * 1e9
     r32 = recs[32]
+    # active network (weights x3, every layer fires): teacher-forced per layer
+    eng3 = vgg16_snn(num_classes=10, pool="max", input_size=32, seed=0, gain=3.0,
+                     engine=True).to(dev)
+    tf = _vgg_teacher_forced(eng3, ov.make_params(0, gain=3.0), recs[32]["img_cpu"], T, dev)
+    spk = [r["agreement"] for r in tf if "agreement" in r]
+    fc3 = [r for r in tf if r["layer"] == "FC3"][0]
+    tf_ok = min(spk) >= 0.999 and fc3["max_abs_logit_err"] < 5e-2
+    del eng3
     rec = {
         "workload": "vgg16", "value": r32["img_s"], "unit": "images/s",
-        "ms_per_step": r32["ms"], "dtype": "bf16 MFMA (fp32 acc), fp32 LIF; fp32 input layer",
+        "ms_per_step": r32["ms"],
+        "dtype": "bf16 MFMA (fp32 acc), fp32 LIF, u1 spikes between layers; fp32 input layer",
         "config": {"workload": "vgg16_snn_32x32_T4_B32_fc512-4096-4096-10", "model": "VGG16-SNN",
                    "T": T, "global_batch": 32, "input": "[B,3,32,32] N(0,1) repeated over T",
                    "output": "mean over T of the logits [B,10], inside the timed graph",
                    "pool": "max", "neuron": "LIF tau=2 theta=1 hard reset 0",
-                   "init": "seeded Kaiming + BN stats (gain 1)"},
+                   "init": "seeded Kaiming + BN stats (gain 1)",
+                   "activations": "packed u32 spike words between conv layers",
+                   "residency": "weights and BN-folded biases (67 MB bf16) are shared by every "
+                                "step and stay resident in the 256 MiB MALL across steps; the "
+                                "inputs rotate over 4 sets; activations (<= 4.2 MB per layer) "
+                                "live in L2/MALL between kernels"},
         "roofline": {"bound": "mfma", "kernel": dom["layer"], "achieved": dom["tflops"],
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": dom["tflops"] / BF16_PEAK_TFLOPS, "traffic": None,
@@ -521,18 +687,28 @@ def bench_vgg(args, dev):
         "layers": layers,
         "batch_curve": [{"B": r["B"], "images_per_s": r["img_s"], "ms_per_forward": r["ms"],
                          "parity": r["parity"]} for r in recs.values()],
-        "parity": all(r["parity"] for r in recs.values()),
+        "parity_checks": {
+            "baseline_init_logits": {
+                "what": "end-to-end mean-over-T logits and argmax vs oracle.vgg.forward at "
+                        "BASELINE's init (gain 1); the deep layers are silent there, so the "
+                        "logits are essentially the FC3 bias (bias-only check)",
+                "pass": all(r["parity"] for r in recs.values())},
+            "gain3_teacher_forced": {
+                "what": "weights x3 (every layer fires), B=32: each layer fed the oracle's "
+                        "input in the engine's format; spike agreement per layer "
+                        "(>= 0.999 required), FC3 max |logit error| (< 5e-2)",
+                "min_spike_agreement": min(spk), "layers": tf, "pass": tf_ok}},
+        "parity": all(r["parity"] for r in recs.values()) and tf_ok,
     }
     _with_traffic(rec["roofline"], "vgg16/" + dom["layer"].split()[0])
     if not args.no_cpu_baseline:
         torch.set_num_threads(cpu_threads())
         img = recs[32]["img_cpu"]
         sec = time_cpu(lambda: ov.forward(params, img, T), budget_s=8.0)
-        rec["cpu_baseline"] = {"value": 32 / sec, "unit": "images/s",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": "oracle.vgg.forward (torch CPU fp32 restatement of "
-                                         "VGGSNN, max-pool) at B=32, T=4",
-                               "seconds_per_call": sec}
+        rec["cpu_baseline"] = cpu_baseline(
+            32 / sec, "images/s",
+            "oracle.vgg.forward (torch CPU fp32 restatement of VGGSNN, max-pool) at B=32, T=4",
+            sec)
     return rec
 
 
@@ -609,11 +785,10 @@ def bench_ssa(args, dev):
         torch.set_num_threads(cpu_threads())
         sec = time_cpu(lambda: oa.ssa_forward(x, p, heads=H, scale=0.125, vth_qkv=1.0,
                                               vth_attn=0.5), budget_s=6.0)
-        rec["cpu_baseline"] = {"value": (B * N) / sec, "unit": "tokens/s (T=4 block)",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": "oracle.attention.ssa_forward (torch CPU fp32 "
-                                         "projections + int64 attention) on the full config",
-                               "seconds_per_call": sec}
+        rec["cpu_baseline"] = cpu_baseline(
+            (B * N) / sec, "tokens/s (T=4 block)",
+            "oracle.attention.ssa_forward (torch CPU fp32 projections + int64 attention) on "
+            "the full config", sec)
     return rec
 
 
@@ -683,14 +858,16 @@ def main():
         "dtype": head["dtype"],
         "data": "synthetic (seeded torch CPU generator), random-init weights",
         "config": {**head["config"], "parallelism": "none (1 GPU)"},
-        **({"layers": head["layers"], "batch_curve": head["batch_curve"],
-            "forward_tflops": head["forward_tflops"]} if "layers" in head else {}),
+        **({k: head[k] for k in ("layers", "batch_curve", "forward_tflops", "parity_checks")
+            if k in head}),
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
         "parity": head["parity"],
         "components": {n: {k: r[k] for k in ("value", "unit", "ms_per_step", "roofline",
                                              "parity", "cpu_baseline", "config", "compare",
-                                             "variants", "pack_A_ms", "pack_A_tbps", "spikes_packed")
+                                             "variants", "pack_A_ms", "pack_A_tbps", "spikes_packed",
+                                             "bytes", "spike_agreement_vs_fp32",
+                                             "packed_equals_bf16_path")
                            if k in r}
                        for n, r in recs.items() if n != names[0]},
     }
