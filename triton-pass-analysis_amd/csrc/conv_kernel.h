@@ -121,6 +121,10 @@ struct ConvArgs {
   // spikes out as packed words (bit c%32 of word c/32 of a pixel's channels,
   // o_tstride in words) instead of bf16 0/1; MODE_LIF without column pooling
   int bits_out;
+  // without split K: deal output tiles to the XCDs Cout-tile major (each XCD
+  // streams its own slice of the weights) instead of row-tile major (each
+  // XCD streams its own rows of x); set where the weights are the larger operand
+  int n_major;
 };
 
 static_assert(offsetof(ConvArgs, x) / 64 == 0 && offsetof(ConvArgs, div_cin) / 64 == 1 &&
@@ -215,8 +219,9 @@ void conv3x3_kernel(ConvArgs a) {
   // Workgroups are dealt to the 8 XCDs round-robin by id; id -> tile is
   // remapped so that each XCD runs one contiguous range of tiles.  Without
   // split-K the range is row-tile major (an XCD's L2 holds its rows'
-  // activations); with split-K it is (split, Cout tile) major, so each XCD
-  // streams its own slice of the weights once.
+  // activations) or, for weight-heavy layers (n_major), Cout-tile major; with
+  // split-K it is (split, Cout tile) major.  Either way the larger operand
+  // is streamed from memory about once rather than once per XCD.
   const int n_mn = a.tiles_m * a.tiles_n;
   const int n_tiles = n_mn * a.splits;
   const int per_xcd = (n_tiles + 7) / 8;
@@ -226,8 +231,13 @@ void conv3x3_kernel(ConvArgs a) {
   // (multiply-high dividers: a runtime integer division is ~30 instructions
   // of straight-line code, fetched cold at the start of every launch)
   if (a.splits == 1) {
-    tm = static_cast<int>(fdiv(static_cast<uint32_t>(tile), a.div_tiles_n));
-    tn = tile - tm * a.tiles_n;
+    if (a.n_major) {
+      tn = static_cast<int>(fdiv(static_cast<uint32_t>(tile), a.div_tiles_m));
+      tm = tile - tn * a.tiles_m;
+    } else {
+      tm = static_cast<int>(fdiv(static_cast<uint32_t>(tile), a.div_tiles_n));
+      tn = tile - tm * a.tiles_n;
+    }
     split = 0;
   } else {
     const int rest = static_cast<int>(fdiv(static_cast<uint32_t>(tile), a.div_tiles_m));
@@ -803,6 +813,7 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
   a.div_tiles_n = make_fastdiv(static_cast<uint32_t>(std::max(1, p.tiles_n)));
   a.splits = p.splits;
   a.stages_per_split = p.stages_per_split;
+  a.n_major = p.splits == 1 && a.w_bytes > a.x_bytes ? 1 : 0;
   a.tickets = static_cast<unsigned int*>(workspace);
   a.partials = p.splits > 1
       ? reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + p.ticket_bytes) : nullptr;
