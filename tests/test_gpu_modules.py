@@ -203,3 +203,81 @@ def test_conv_pool_dense_weights_follow_state_dict():
         conv2.bias.zero_()
     fresh = FusedConvBNLIFPool(conv2.eval(), None, pool="max").to(DEV)
     assert torch.equal(fresh(x), y2)
+
+
+def _spikes(shape, seed, p=0.2):
+    return (torch.rand(*shape, generator=torch.Generator().manual_seed(seed)) < p).float()
+
+
+def _membrane_near(y, bias, neuron, soft, v_reset, tol=2e-2):
+    """Steps at which the fp32 membrane (CPU oracle, fed the conv output y) is
+    within tol of the threshold, at that step or earlier."""
+    from oracle.fused import membrane_trace
+    tr = membrane_trace(y, bias=bias, neuron=neuron, tau=2.0, soft_reset=soft,
+                        v_threshold=1.0, v_reset=v_reset)
+    near = (tr - 1.0).abs() < tol
+    return torch.cummax(near.int(), 0).values.bool()
+
+
+@pytest.mark.parametrize("neuron,soft,v_reset", [("lif", False, 0.0), ("if", True, 0.0),
+                                                 ("lif", True, 0.2)])
+@pytest.mark.parametrize("layout", ["NCHW", "NHWC"])
+def test_conv_bn_neuron_bf16_runs_the_hip_conv(neuron, soft, v_reset, layout):
+    """FusedConvBNNeuron (BN folded) on bf16 spikes with a 3x3 conv runs the
+    HIP implicit-GEMM conv with the neuron in its epilogue: the same spikes as
+    FusedConvBNLIFPool without a pool (same kernel), >= 99.9% agreement with
+    the fp32 conv + oracle neuron with every flip near threshold, and the
+    module's layout contract (channels-last memory for 'NHWC')."""
+    from snnk.nn import FusedConvBNNeuron, FusedConvBNLIFPool
+    from oracle.fused import fold_conv_bn, conv3x3_seq
+    torch.manual_seed(0)
+    conv = nn.Conv2d(64, 96, 3, padding=1)
+    bn = nn.BatchNorm2d(96).eval()
+    with torch.no_grad():
+        conv.weight.mul_(2.0)
+        bn.running_mean.uniform_(-0.1, 0.1)
+        bn.running_var.uniform_(0.5, 1.5)
+    kw = dict(neuron=neuron, tau=2.0, soft_reset=soft, v_threshold=1.0, v_reset=v_reset)
+    mod = FusedConvBNNeuron(conv, bn, fold_bn=True, layout=layout, **kw).to(DEV)
+    x = _spikes((4, 2, 64, 10, 6), 21)
+    got = mod(x.to(DEV, torch.bfloat16))
+    assert got.dtype == torch.bfloat16 and got.shape == (4, 2, 96, 10, 6)
+    if layout == "NHWC":
+        assert got[0].is_contiguous(memory_format=torch.channels_last)
+    else:
+        assert got.is_contiguous()
+    pool = FusedConvBNLIFPool(conv, bn, pool=None, **kw).to(DEV)
+    assert torch.equal(got, pool(x.to(DEV, torch.bfloat16)))
+    w2, b2 = fold_conv_bn(conv.weight.detach(), conv.bias.detach(), bn.weight.detach(),
+                          bn.bias.detach(), bn.running_mean, bn.running_var, bn.eps)
+    y = conv3x3_seq(x, w2)
+    ref, _, _ = on.lif_multistep(y, bias=b2, neuron=neuron, tau=2.0, soft_reset=soft,
+                                 v_threshold=1.0, v_reset=v_reset)
+    g = got.float().cpu()
+    assert (g == ref).float().mean().item() >= 0.999
+    assert not torch.any((g != ref) & ~_membrane_near(y, b2, neuron, soft, v_reset))
+    # fp32 input keeps the vendor conv in fp32, then the HIP neuron: the
+    # oracle's neuron on the same conv output is bit-equal to it
+    mod.conv_mfma = False
+    got32 = mod(x.to(DEV)).cpu()
+    assert (got32 == ref).float().mean().item() >= 0.999
+
+
+def test_conv_neuron_bf16_runs_the_hip_conv_and_opt_out():
+    """FusedConvNeuron with bias on bf16 spikes: the HIP conv path equals the
+    vendor path (conv_mfma=False, bf16 conv + HIP neuron) up to near-threshold
+    flips; shapes outside the kernel (5x5, Cin % 32 != 0) keep the vendor conv."""
+    from snnk.nn import FusedConvNeuron
+    torch.manual_seed(1)
+    mod = FusedConvNeuron(32, 64, 3, padding=1, neuron="lif", tau=2.0).to(DEV)
+    with torch.no_grad():
+        mod.weight.mul_(3.0)
+    x = _spikes((4, 4, 32, 8, 8), 31).to(DEV, torch.bfloat16)
+    hip = mod(x).float()
+    mod.conv_mfma = False
+    vendor = mod(x).float()
+    assert (hip == vendor).float().mean().item() >= 0.999
+    odd = FusedConvNeuron(32, 64, 5, padding=2, neuron="lif").to(DEV)
+    assert odd(x).shape == (4, 4, 64, 8, 8)
+    narrow = FusedConvNeuron(3, 64, 3, padding=1, neuron="lif").to(DEV)
+    assert narrow(_spikes((4, 2, 3, 8, 8), 32).to(DEV, torch.bfloat16)).shape == (4, 2, 64, 8, 8)

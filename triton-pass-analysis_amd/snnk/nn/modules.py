@@ -126,6 +126,24 @@ class _NeuronArgs:
         self.soft_reset, self.v_reset, self.layout = soft_reset, v_reset, layout
         _thr(self, v_threshold)
 
+    def _mfma_conv(self, x_seq, weight, bias):
+        """conv3x3 + bias + neuron in one HIP kernel (bf16 MFMA, fp32
+        accumulation) on bf16 spikes; returns [T, B, C, H, W] bf16, in
+        channels-last memory for layout 'NHWC'.  The bf16 weight matrix is
+        rebuilt whenever ``weight`` is replaced or changed in place."""
+        stamp = (weight.device, weight.data_ptr(), weight._version)
+        hit = self.__dict__.get("_w_prep_cache")
+        if hit is None or hit[0] != stamp:
+            hit = (stamp, prepare_conv3x3_weight(weight.detach().float()))
+            self.__dict__["_w_prep_cache"] = hit
+        df, sc = neuron_params(self.neuron, self.tau, self.decay, self.decay_input)
+        b = None if bias is None else bias.detach().float().contiguous()
+        s = conv3x3_bn_lif_nhwc(to_nhwc_bf16(x_seq), hit[1], b, pool=False, decay=df,
+                                in_scale=sc, v_threshold=float(self.v_threshold),
+                                v_reset=self.v_reset, soft_reset=self.soft_reset)
+        s = s.permute(0, 1, 4, 2, 3)
+        return s if self.layout == "NHWC" else s.contiguous()
+
     def _lif(self, y_seq, bias, residual=None):
         return fused_bias_if_lif(
             y_seq, bias, residual=residual, neuron=self.neuron, tau=self.tau,
@@ -133,10 +151,25 @@ class _NeuronArgs:
             v_threshold=self.v_threshold, v_reset=self.v_reset, layout=self.layout)
 
 
+def _mfma_conv_fits(x_seq, weight, conv, v_threshold) -> bool:
+    """bf16 input to a 3x3 / stride 1 / padding 1 conv with channel counts
+    that are multiples of 32 and a float threshold: what the HIP implicit-GEMM
+    conv + neuron kernel covers."""
+    return (x_seq.is_cuda and x_seq.dtype == torch.bfloat16 and x_seq.ndim == 5
+            and tuple(weight.shape[2:]) == (3, 3) and conv["groups"] == 1
+            and tuple(conv["stride"]) == (1, 1) and tuple(conv["padding"]) == (1, 1)
+            and tuple(conv["dilation"]) == (1, 1)
+            and weight.shape[0] % 32 == 0 and weight.shape[1] % 32 == 0
+            and not isinstance(v_threshold, torch.Tensor))
+
+
 def _conv_seq(x_seq, w, bias, conv, layout):
     """Vendor conv over [T*B, ...] returning [T, B, ...] in the module's layout."""
     T, B = x_seq.shape[0], x_seq.shape[1]
     x4 = x_seq.reshape(T * B, *x_seq.shape[2:])
+    # the conv runs in the input's dtype (fp32 parameters meet a bf16 input)
+    w = w.to(x4.dtype)
+    bias = None if bias is None else bias.to(x4.dtype)
     if layout == "NHWC":
         x4 = x4.contiguous(memory_format=torch.channels_last)
         w = w.to(memory_format=torch.channels_last)
@@ -152,8 +185,13 @@ def _conv_seq(x_seq, w, bias, conv, layout):
 
 
 class FusedConvNeuron(nn.Module, _NeuronArgs):
-    """Conv2d (vendor, no bias) + bias + IF/LIF in one HIP kernel
-    (snn_compiler/nn/modules.py:160-217)."""
+    """Conv2d + bias + IF/LIF (snn_compiler/nn/modules.py:160-217).
+
+    A bf16 input to a 3x3 / stride 1 / padding 1 conv with channel counts that
+    are multiples of 32 (float threshold) runs the HIP implicit-GEMM conv with
+    the bias and the neuron in its epilogue.  Other shapes -- and always fp32
+    inputs, keeping the reference's precision -- run the vendor conv in the
+    input's dtype, then the HIP neuron kernel."""
 
     def __init__(self, in_ch, out_ch, kernel_size, *, stride=1, padding=0, dilation=1,
                  groups=1, bias: bool = True, neuron: str = "if", tau: float = 2.0,
@@ -169,8 +207,11 @@ class FusedConvNeuron(nn.Module, _NeuronArgs):
                          groups=conv.groups)
         self._set_neuron(neuron, tau, decay, decay_input, soft_reset, v_threshold, v_reset,
                          layout)
+        self.conv_mfma = True  # False: the vendor conv for every input
 
     def forward(self, x_seq):
+        if self.conv_mfma and _mfma_conv_fits(x_seq, self.weight, self.conv, self.v_threshold):
+            return self._mfma_conv(x_seq, self.weight, self.bias)
         y = _conv_seq(x_seq, self.weight, None, self.conv, self.layout)
         b = None if self.bias is None else self.bias.float().contiguous()
         return self._lif(y, b)
@@ -217,9 +258,12 @@ class FusedLinearNeuron(nn.Module, _NeuronArgs):
 class FusedConvBNNeuron(nn.Module, _NeuronArgs):
     """Conv2d + eval BN + IF/LIF (snn_compiler/nn/modules.py:258-357).
 
-    fold_bn=True folds BN into the conv once; fold_bn=False keeps conv and BN
-    as separate vendor ops (bit-exact with the unfused network) and fuses
-    only the neuron.
+    fold_bn=True folds BN into the conv once; a bf16 input to a 3x3 / stride 1
+    / padding 1 conv with channel counts that are multiples of 32 then runs
+    the HIP implicit-GEMM conv with the folded bias and the neuron in its
+    epilogue, other shapes and fp32 inputs the vendor conv then the HIP
+    neuron kernel.  fold_bn=False keeps conv and BN as separate vendor ops
+    (bit-exact with the unfused network) and fuses only the neuron.
     """
 
     def __init__(self, conv: nn.Conv2d, bn: nn.BatchNorm2d, *, fold_bn: bool = True,
@@ -249,6 +293,7 @@ class FusedConvBNNeuron(nn.Module, _NeuronArgs):
                          groups=conv.groups)
         self._set_neuron(neuron, tau, decay, decay_input, soft_reset, v_threshold, v_reset,
                          layout)
+        self.conv_mfma = True  # False: the vendor conv for every input
 
     def _conv_bn(self, x_seq):
         if self.fold_bn:
@@ -263,6 +308,9 @@ class FusedConvBNNeuron(nn.Module, _NeuronArgs):
         return y4.view(T, B, *y4.shape[1:]), None
 
     def forward(self, x_seq):
+        if self.fold_bn and self.conv_mfma and \
+                _mfma_conv_fits(x_seq, self.weight, self.conv, self.v_threshold):
+            return self._mfma_conv(x_seq, self.weight, self.bias)
         y, bias = self._conv_bn(x_seq)
         return self._lif(y, bias)
 

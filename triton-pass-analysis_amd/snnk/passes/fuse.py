@@ -199,15 +199,22 @@ def _build_conv3x3_mfma(run, opt):
     return build_conv_lif_pool(conv, bn, NeuronSpec.of(run[k]), pool=len(run) > k + 1)
 
 
+def _mfma_opt(mod: nn.Module, opt: Options) -> nn.Module:
+    """conv_mfma=False keeps the module's bf16 path on the vendor conv too."""
+    mod.conv_mfma = opt.conv_mfma
+    return mod
+
+
 RULES: Tuple[Rule, ...] = (
     Rule("conv3x3_mfma", _match_conv3x3_mfma, _build_conv3x3_mfma),
     Rule("conv_bn",
          lambda L, i, o: 3 if (_at(L, i, nn.Conv2d) and _at(L, i + 1, nn.BatchNorm2d)
                                and _at(L, i + 2, _is_neuron)) else 0,
-         lambda r, o: build_conv_bn_neuron(r[0], r[1], NeuronSpec.of(r[2]), o.layout, o.fold_bn)),
+         lambda r, o: _mfma_opt(build_conv_bn_neuron(r[0], r[1], NeuronSpec.of(r[2]), o.layout,
+                                                     o.fold_bn), o)),
     Rule("conv",
          lambda L, i, o: 2 if (_at(L, i, nn.Conv2d) and _at(L, i + 1, _is_neuron)) else 0,
-         lambda r, o: build_conv_neuron(r[0], NeuronSpec.of(r[1]), o.layout)),
+         lambda r, o: _mfma_opt(build_conv_neuron(r[0], NeuronSpec.of(r[1]), o.layout), o)),
     Rule("linear",
          lambda L, i, o: 2 if (_at(L, i, nn.Linear) and _at(L, i + 1, _is_neuron)) else 0,
          lambda r, o: build_linear_neuron(r[0], NeuronSpec.of(r[1]))),
