@@ -185,6 +185,10 @@ def fold_conv_bn(conv_w, conv_b, bn_w, bn_b, bn_mean, bn_var, bn_eps):
     return new_w, new_b
 
 
+def _pair(v) -> tuple:
+    return tuple(v) if isinstance(v, (tuple, list)) else (v, v)
+
+
 def conv_neuron(
     x_seq: torch.Tensor,
     weight: torch.Tensor,
@@ -200,12 +204,29 @@ def conv_neuron(
     v_reset: float = 0.0,
     layout: str = "NCHW",
 ) -> torch.Tensor:
-    """Vendor conv (MIOpen, no bias) then the fused bias+neuron HIP kernel.
+    """Conv (no bias) then the fused bias+neuron HIP kernel.
 
-    Reference: snn_compiler/kernels/fused.py:513-551.  The fused
-    conv3x3 + BN + LIF + max-pool MFMA kernel is :func:`snnk.kernels.conv.conv_bn_lif_pool`.
+    Reference: snn_compiler/kernels/fused.py:513-551.  A bf16 input to a 3x3 /
+    stride 1 / padding 1 conv with channel counts that are multiples of 32
+    (float threshold) runs the HIP implicit-GEMM conv with the bias and the
+    neuron in its epilogue; otherwise the vendor conv (MIOpen) runs in the
+    input's dtype.  The conv3x3 + BN + LIF + max-pool kernel is
+    :func:`snnk.kernels.conv.conv_bn_lif_pool`.
     """
     T, B = x_seq.shape[0], x_seq.shape[1]
+    if (x_seq.is_cuda and x_seq.dtype == torch.bfloat16 and x_seq.ndim == 5
+            and tuple(weight.shape[2:]) == (3, 3) and groups == 1
+            and _pair(stride) == (1, 1) and _pair(padding) == (1, 1) and _pair(dilation) == (1, 1)
+            and weight.shape[0] % 32 == 0 and weight.shape[1] % 32 == 0
+            and not isinstance(v_threshold, torch.Tensor)):
+        from .conv import conv3x3_bn_lif_nhwc, prepare_conv3x3_weight, to_nhwc_bf16
+        df, sc = neuron_params(neuron, tau, decay, decay_input)
+        b = None if bias is None else bias.detach().float().contiguous()
+        s = conv3x3_bn_lif_nhwc(to_nhwc_bf16(x_seq), prepare_conv3x3_weight(weight.float()), b,
+                                pool=False, decay=df, in_scale=sc, v_threshold=float(v_threshold),
+                                v_reset=v_reset, soft_reset=soft_reset).permute(0, 1, 4, 2, 3)
+        return s if layout == "NHWC" else s.contiguous()
+    weight = weight.to(x_seq.dtype)
     x_4d = x_seq.reshape(T * B, *x_seq.shape[2:])
     if layout == "NHWC":
         x_4d = x_4d.contiguous(memory_format=torch.channels_last)
@@ -234,12 +255,24 @@ def linear_neuron(
     v_threshold=1.0,
     v_reset: float = 0.0,
 ) -> torch.Tensor:
-    """Vendor GEMM (no bias) then the fused bias+neuron HIP kernel.
+    """GEMM (no bias) then the fused bias+neuron HIP kernel.
 
-    Reference: snn_compiler/kernels/fused.py:554-579.
+    Reference: snn_compiler/kernels/fused.py:554-579.  A bf16 input whose
+    shapes the fused kernel covers (features multiples of 32, batch a
+    multiple of 4, float threshold) runs the bf16-MFMA GEMM with the bias and
+    the neuron in its epilogue; otherwise the vendor GEMM runs in the input's
+    dtype.
     """
     T, B = x_seq.shape[0], x_seq.shape[1]
-    y = F.linear(x_seq.reshape(T * B, -1), weight, bias=None)
+    from .linear import linear_bias_lif, linear_fusable
+    if x_seq.dtype == torch.bfloat16 and linear_fusable(x_seq, weight, v_threshold):
+        df, sc = neuron_params(neuron, tau, decay, decay_input)
+        b = None if bias is None else bias.detach().float().contiguous()
+        return linear_bias_lif(x_seq.reshape(T, B, -1).contiguous(),
+                               weight.detach().to(torch.bfloat16).contiguous(), b, decay=df,
+                               in_scale=sc, v_threshold=float(v_threshold), v_reset=v_reset,
+                               soft_reset=soft_reset)
+    y = F.linear(x_seq.reshape(T * B, -1), weight.to(x_seq.dtype), bias=None)
     y_seq = y.view(T, B, y.shape[-1])
     return fused_bias_if_lif(
         y_seq, bias, neuron=neuron, tau=tau, decay=decay,
