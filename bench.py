@@ -341,7 +341,12 @@ def bench_bgemm(args, dev):
                      "achieved": achieved, "peak": peak, "unit": "TOPS",
                      "frac": achieved / peak, "traffic": None,
                      "algorithmic_ops": ops, "kernel_ms_mean": kern_ms,
-                     "peak_note": note},
+                     "peak_note": note,
+                     "vs_int8_peak": {"peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                                      "frac": achieved / INT8_PEAK_TOPS,
+                                      "note": "BASELINE's roofline for this config is the "
+                                              "dense int8 MFMA peak; the kernel issues MX "
+                                              "fp4 MFMAs, whose peak is the one in 'peak'"}},
         "compare": {"algo": other, "kernel": kinds[other][0], "kernel_ms_mean": other_ms,
                     "achieved": other_tops, "peak": kinds[other][1],
                     "frac": other_tops / kinds[other][1]},
