@@ -721,8 +721,14 @@ def bench_vgg(args, dev):
 # Spike self-attention block
 # --------------------------------------------------------------------------
 def bench_ssa(args, dev):
-    from snnk.kernels.attention import spike_attention
-    from snnk.kernels.linear import linear_bias_lif, linear_preact
+    """The SSA block on packed spikes (input, Q/K/V and attention spikes as
+    packed words, every head on whole words; fp32 output), with the bf16-spike
+    block timed beside it."""
+    from snnk.kernels.attention import (spike_attention, spike_attention_packed,
+                                        prepare_ssa_packed)
+    from snnk.kernels.binary import pack_bits
+    from snnk.kernels.linear import (linear_bias_lif, linear_bias_lif_act, linear_preact,
+                                     linear_preact_act)
     from oracle import attention as oa
 
     T, B, N, D, H = 4, 32, 64, 384, 8
@@ -733,57 +739,104 @@ def bench_ssa(args, dev):
     w_qkv = torch.cat([p["wq"], p["wk"], p["wv"]]).to(dev, torch.bfloat16).contiguous()
     b_qkv = torch.cat([p["bq"], p["bk"], p["bv"]]).to(dev).contiguous()
     w_p, b_p = p["wp"].to(dev, torch.bfloat16).contiguous(), p["bp"].to(dev).contiguous()
+    prep = prepare_ssa_packed(w_qkv, b_qkv, w_p, heads=H)
+    d, slot = D // H, prep["slot"]
+    hw, Hw = slot // 32, H * slot // 32
     nsets = 8
-    xs = [x.to(dev, torch.bfloat16).reshape(T, B * N, D).contiguous() for _ in range(nsets)]
+    x_bf = x.to(dev, torch.bfloat16).reshape(T, B * N, D).contiguous()
+    xs = [x_bf.clone() for _ in range(nsets)]
+    xws = [pack_bits(x_bf, dim=-1) for _ in range(nsets)]
     qkvs = [torch.empty(T, B * N, 3 * D, device=dev, dtype=torch.bfloat16) for _ in range(nsets)]
     attns = [torch.empty(T, B * N, D, device=dev, dtype=torch.bfloat16) for _ in range(nsets)]
+    qkvw = [torch.empty(T, B * N, 3 * D // 32, device=dev, dtype=torch.int32) for _ in range(nsets)]
+    attnw = [torch.empty(T, B * N, Hw, device=dev, dtype=torch.int32) for _ in range(nsets)]
     outs = [torch.empty(T, B * N, D, device=dev) for _ in range(nsets)]
     lif = dict(decay=0.5, in_scale=0.5, v_threshold=1.0)
 
+    # packed block
     def proj_qkv(i):
-        linear_bias_lif(xs[i], w_qkv, b_qkv, out=qkvs[i], **lif)
+        linear_bias_lif_act(xws[i], prep["w_qkv"], prep["b_qkv"], out=qkvw[i], out_bits=True, **lif)
+
+    Dw = D // 32
 
     def attention(i):
-        q = qkvs[i]
-        spike_attention(q[..., :D], q[..., D:2 * D], q[..., 2 * D:], B=B, N=N, heads=H,
-                        scale=0.125, v_threshold=0.5, out=attns[i])
+        q = qkvw[i]
+        spike_attention_packed(q[..., :Dw], q[..., Dw:2 * Dw], q[..., 2 * Dw:], B=B, N=N, heads=H,
+                               d=d, in_head_bits=d, out_head_words=hw, scale=0.125,
+                               v_threshold=0.5, out=attnw[i])
 
     def proj_out(i):
-        linear_preact(attns[i], w_p, b_p, out=outs[i])
+        linear_preact_act(attnw[i], prep["w_proj"], b_p, out=outs[i])
 
     def step(i):
         proj_qkv(i)
         attention(i)
         proj_out(i)
 
+    # bf16 block
+    def proj_qkv_bf(i):
+        linear_bias_lif(xs[i], w_qkv, b_qkv, out=qkvs[i], **lif)
+
+    def attention_bf(i):
+        q = qkvs[i]
+        spike_attention(q[..., :D], q[..., D:2 * D], q[..., 2 * D:], B=B, N=N, heads=H,
+                        scale=0.125, v_threshold=0.5, out=attns[i])
+
+    def proj_out_bf(i):
+        linear_preact(attns[i], w_p, b_p, out=outs[i])
+
+    def step_bf(i):
+        proj_qkv_bf(i)
+        attention_bf(i)
+        proj_out_bf(i)
+
     wall, _ = time_gpu(step, nsets, args.steps, args.warmup)
     _, ms_qkv = time_gpu(proj_qkv, nsets, args.steps, args.warmup)
     _, ms_att = time_gpu(attention, nsets, args.steps, args.warmup)
     _, ms_out = time_gpu(proj_out, nsets, args.steps, args.warmup)
+    wall_bf, _ = time_gpu(step_bf, nsets, args.steps, args.warmup)
+    _, ms_qkv_bf = time_gpu(proj_qkv_bf, nsets, args.steps, args.warmup)
+    _, ms_att_bf = time_gpu(attention_bf, nsets, args.steps, args.warmup)
+    _, ms_out_bf = time_gpu(proj_out_bf, nsets, args.steps, args.warmup)
     fl_qkv = 2.0 * T * B * N * D * 3 * D
     fl_out = 2.0 * T * B * N * D * D
     ops_att = 2.0 * 2 * T * B * H * N * N * (D // H)
     ref = oa.ssa_forward(x, p, heads=H, scale=0.125, vth_qkv=1.0, vth_attn=0.5)
-    qkv_agree = (qkvs[0].cpu().float().view(T, B, N, 3 * D)
-                 == torch.cat([ref["q"], ref["k"], ref["v"]], -1)).float().mean().item()
-    kern = [("qkv_projection_lif", ms_qkv, fl_qkv, BF16_PEAK_TFLOPS, "TFLOP/s"),
-            ("attention_core_lif", ms_att, ops_att, INT8_PEAK_TOPS, "TOPS"),
-            ("output_projection", ms_out, fl_out, BF16_PEAK_TFLOPS, "TFLOP/s")]
+    # packed Q/K/V back to [T, B*N, 3D] 0/1
+    bits = (qkvw[0].unsqueeze(-1) >> torch.arange(32, device=dev)) & 1
+    qkv_unp = bits.reshape(T, B, N, 3 * D).float().cpu()
+    qkv_agree = (qkv_unp == torch.cat([ref["q"], ref["k"], ref["v"]], -1)).float().mean().item()
+    same_qkv = bool(torch.equal(qkv_unp.view(T, B * N, 3 * D), qkvs[0].float().cpu()))
+    abits = (attnw[0].unsqueeze(-1) >> torch.arange(32, device=dev)) & 1
+    attn_unp = abits.reshape(T, B * N, H, slot)[..., :d].reshape(T, B * N, D).float()
+    same_attn = bool(torch.equal(attn_unp, attns[0].float()))
+    # algorithmic work of the block as the reference defines it (unpadded)
+    kern = [("qkv_projection_lif (packed spikes in and out)", ms_qkv, fl_qkv, BF16_PEAK_TFLOPS, "TFLOP/s"),
+            ("attention_core_lif (packed)", ms_att, ops_att, INT8_PEAK_TOPS, "TOPS"),
+            ("output_projection (packed spikes in)", ms_out, fl_out, BF16_PEAK_TFLOPS, "TFLOP/s")]
     per = [{"kernel": k, "kernel_ms": ms, "achieved": w / (ms * 1e-3) / 1e12, "peak": pk,
             "unit": u, "frac": w / (ms * 1e-3) / 1e12 / pk} for k, ms, w, pk, u in kern]
     dom = max(per, key=lambda r: r["kernel_ms"])
     rec = {
         "workload": "ssa", "value": (B * N) / wall, "unit": "tokens/s (T=4 block)",
-        "ms_per_step": wall * 1e3, "dtype": "bf16 projections (fp32 acc), int8 attention, fp32 LIF",
+        "ms_per_step": wall * 1e3,
+        "dtype": "bf16 projections (fp32 acc), int8 attention, fp32 LIF; u1 spikes",
         "config": {"workload": "spike_self_attention_T4_B32_N64_D384_H8", "T": T, "B": B,
-                   "N": N, "D": D, "heads": H, "scale": 0.125, "vth_qkv": 1.0, "vth_attn": 0.5},
+                   "N": N, "D": D, "heads": H, "scale": 0.125, "vth_qkv": 1.0, "vth_attn": 0.5,
+                   "spikes": "packed u32 words: input, Q/K/V (heads back to back), attention "
+                             f"spikes (each head on {slot} bits); fp32 output"},
         "roofline": {"bound": "mfma", "kernel": dom["kernel"], "achieved": dom["achieved"],
                      "peak": dom["peak"], "unit": dom["unit"], "frac": dom["frac"],
                      "traffic": None, "kernel_ms_mean": dom["kernel_ms"]},
         "kernels": per,
+        "variants": {"bf16_spikes": {
+            "value": (B * N) / wall_bf, "ms_per_step": wall_bf * 1e3,
+            "kernels_ms": {"qkv_projection_lif": ms_qkv_bf, "attention_core_lif": ms_att_bf,
+                           "output_projection": ms_out_bf}}},
         "block_gops": (fl_qkv + fl_out + ops_att) / 1e9,
         "qkv_spike_agreement_vs_fp32": qkv_agree,
-        "parity": qkv_agree >= 0.999,
+        "packed_equals_bf16_path": same_qkv and same_attn,
+        "parity": qkv_agree >= 0.999 and same_qkv and same_attn,
     }
     _with_traffic(rec["roofline"], "ssa")
     if not args.no_cpu_baseline:
@@ -863,7 +916,10 @@ def main():
         "dtype": head["dtype"],
         "data": "synthetic (seeded torch CPU generator), random-init weights",
         "config": {**head["config"], "parallelism": "none (1 GPU)"},
-        **({k: head[k] for k in ("layers", "batch_curve", "forward_tflops", "parity_checks")
+        **({k: head[k] for k in ("layers", "batch_curve", "forward_tflops", "parity_checks",
+                                 "kernels", "variants", "compare", "bytes",
+                                 "spike_agreement_vs_fp32", "qkv_spike_agreement_vs_fp32",
+                                 "packed_equals_bf16_path", "spikes_packed")
             if k in head}),
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
@@ -872,7 +928,8 @@ def main():
                                              "parity", "cpu_baseline", "config", "compare",
                                              "variants", "pack_A_ms", "pack_A_tbps", "spikes_packed",
                                              "bytes", "spike_agreement_vs_fp32",
-                                             "packed_equals_bf16_path")
+                                             "packed_equals_bf16_path", "kernels",
+                                             "qkv_spike_agreement_vs_fp32")
                            if k in r}
                        for n, r in recs.items() if n != names[0]},
     }

@@ -286,6 +286,17 @@ int snnk_linear_bias_lif_act(const void* x, int32_t x_fmt, const uint16_t* w, co
                              float in_scale, float v_threshold, float v_reset,
                              int32_t soft_reset, int32_t tile_hint, int32_t splits,
                              void* workspace, int64_t workspace_bytes, void* stream);
+/* Pre-activation Linear on packed or bf16 spike rows: out [T][R][N] fp32 =
+ * x W^T + bias (no neuron), x as in snnk_linear_bias_lif_act (x_fmt).  Size
+ * the workspace with snnk_linear_bias_lif_act_ws_size (col_pool 0).
+ * Replaces the output projection of the SSA block
+ * (snn_compiler/nn/attention.py:160-164: proj_linear on the attention
+ * spikes) when those spikes arrive packed. */
+int snnk_linear_preact_act(const void* x, int32_t x_fmt, const uint16_t* w, const float* bias,
+                           float* out, int64_t T, int64_t R, int64_t K, int64_t N,
+                           int32_t tile_hint, int32_t splits, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
 /* Workspace bytes of the _act calls (packed x has its own tile / split plan,
  * so its workspace may differ from the bf16 one); col_pool as in
  * snnk_linear_bias_lif_pool4_ws (bf16 spikes out). */
@@ -382,6 +393,28 @@ int snnk_spike_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v
  * integer kv (sums below 2^24) gives the exact count; real kv gives an fp32
  * sum.  q values other than 0/1 are rounded to bf16.
  */
+/*
+ * snnk_spike_attention on packed spikes: q, k, v and the output are uint32
+ * words of LSB-first bits (the _pack_N convention).  Head h of q, k and v
+ * starts at bit h*in_head_bits of a token row (in_head_bits >= d, a multiple
+ * of 8: in_head_bits = d reads the rows a packed projection writes); head h
+ * of the output starts at word h*out_head_words (>= ceil(d/32)), its bits
+ * past d written as zero.  Row and step strides count words; 4-byte
+ * alignment.  N <= 64 and d <= 64 (the quadratic core).  The same counts and
+ * spikes as snnk_spike_attention.  Replaces the same reference code as
+ * snnk_spike_attention (snn_compiler/nn/attention.py:133-164), on the packed
+ * format of _pack_N (snn_compiler/kernels/attention.py:195-214).
+ */
+int snnk_spike_attention_packed(const uint32_t* q, const uint32_t* k, const uint32_t* v,
+                                int64_t q_row, int64_t k_row, int64_t v_row,
+                                int64_t q_step, int64_t k_step, int64_t v_step,
+                                int64_t in_head_bits, uint32_t* spikes_out,
+                                int64_t out_row, int64_t out_step, int64_t out_head_words,
+                                int32_t* s_counts, int32_t* o_counts,
+                                int64_t T, int64_t B, int64_t H, int64_t N, int64_t d,
+                                float decay, float in_scale, float v_threshold,
+                                float v_reset, int32_t soft_reset, void* stream);
+
 int snnk_spike_av_lif(const void* q, int32_t q_dtype, const void* kv, int32_t kv_dtype,
                       void* spikes_out, int64_t T, int64_t BH, int64_t N, int64_t d,
                       float decay, float in_scale, float v_threshold, float v_reset,

@@ -52,7 +52,19 @@ struct AttnArgs {
   int soft_reset;
   int o_vec;  // output rows and steps 8-byte aligned: 4 spikes per store
   int per_xcd;  // (batch, head) blocks per XCD
+  // packed spikes (PK kernels): q, k, v and out are uint32 words of LSB-first
+  // bits; head h of q, k, v starts at bit h*hbits of a row (a multiple of 8,
+  // so 8 dims never straddle a word), head h of out at word h*ohw; row and
+  // step strides count words
+  int hbits, ohw;
 };
+
+// 8 spikes (bits of b, LSB first) -> 8 int8 0/1: each nibble times
+// 0x00204081 puts its bit i at bit 8*i + ... with no overlap, and the mask
+// keeps bit 0 of every byte.
+__device__ __forceinline__ u32x2 bits_to_bytes8(uint32_t b) {
+  return u32x2{((b & 0xFu) * 0x00204081u) & 0x01010101u, (((b >> 4) & 0xFu) * 0x00204081u) & 0x01010101u};
+}
 
 // Nonzero test of the two bf16 in a word, sign ignored: bit 15 (31) of the
 // result is set iff the low (high) element is nonzero -- each 15-bit
@@ -88,7 +100,8 @@ static_assert(kMaxTok == kMaxDim, "Q, K, V^T and S share one staging size");
 static_assert(kMaxTok * (kMaxDim / 8) == 2 * kStagers, "two Q/K chunks per stager");
 static_assert((kMaxTok / 4) * (kMaxDim / 2) == 2 * kStagers, "two V patches per stager");
 
-template <int NT, int DT, bool SR>  // token tiles, dim tiles (32 each), soft reset
+// token tiles, dim tiles (32 each), soft reset, packed spikes in and out
+template <int NT, int DT, bool SR, bool PK>
 __global__ __launch_bounds__(kThreads) void ssa_attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t qs[2 * kStage];
   __shared__ __attribute__((aligned(16))) int8_t ks[2 * kStage];
@@ -108,9 +121,17 @@ __global__ __launch_bounds__(kThreads) void ssa_attention_kernel(AttnArgs a) {
   const int r32 = lane & 31, g = lane >> 5;
   // this block's (batch, head) slice: token row 0, column h*d
   const int64_t row0 = static_cast<int64_t>(b) * a.N;
-  const uint16_t* qb = a.q + row0 * a.q_row + h * a.d;
-  const uint16_t* kb = a.k + row0 * a.k_row + h * a.d;
-  const uint16_t* vb = a.v + row0 * a.v_row + h * a.d;
+  // the block's first token row (packed: the head's bit offset goes into the
+  // per-thread offsets) or its head's first element (bf16)
+  const int64_t hcol = PK ? 0 : static_cast<int64_t>(h) * a.d;
+  const int hbit0 = PK ? h * a.hbits : 0;
+  const uint16_t* qb = PK ? reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint32_t*>(a.q) + row0 * a.q_row)
+                          : a.q + row0 * a.q_row + hcol;
+  const uint16_t* kb = PK ? reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint32_t*>(a.k) + row0 * a.k_row)
+                          : a.k + row0 * a.k_row + hcol;
+  const uint16_t* vb = PK ? reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint32_t*>(a.v) + row0 * a.v_row)
+                          : a.v + row0 * a.v_row + hcol;
+  constexpr int kElem = PK ? 4 : 2;  // bytes per stride unit
 
   const bool stager = wave >= 4;
   const bool has_s = stager && wave - 4 < NT * NT;
@@ -119,7 +140,9 @@ __global__ __launch_bounds__(kThreads) void ssa_attention_kernel(AttnArgs a) {
   const int oi = wave / DT, od = wave % DT;
   // O^T accumulator of this lane: token oi*32 + r32, dims od*32 + 8*(e/4) + 4*g + e%4
   const int ti = oi * 32 + r32;
-  uint16_t* ob = a.out + (row0 + ti) * a.o_row + h * a.d;
+  uint16_t* ob = a.out + (row0 + ti) * a.o_row + h * a.d;  // (bf16 output)
+  uint32_t* obw = reinterpret_cast<uint32_t*>(a.out) + (row0 + ti) * a.o_row +
+                  static_cast<int64_t>(h) * a.ohw;  // (packed)
   float vm[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) vm[e] = 0.0f;
@@ -135,29 +158,45 @@ __global__ __launch_bounds__(kThreads) void ssa_attention_kernel(AttnArgs a) {
   constexpr uint32_t kOutside = 0x80000000u;  // > kRecords
   constexpr int kRecords = 0x7FFFFFFF;
   uint32_t qoff[2], koff[2], voff[2][4];
+  uint32_t qsh[2], vsh[2];  // packed: bit position of the chunk / dim pair in its word
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     const int c = st + kStagers * m;
     const int qn = c >> 3, qc = c & 7;
     const bool in = qn < a.N && qc * 8 < a.d;
-    qoff[m] = in ? static_cast<uint32_t>((qn * a.q_row + qc * 8) * 2) : kOutside;
-    koff[m] = in ? static_cast<uint32_t>((qn * a.k_row + qc * 8) * 2) : kOutside;
+    // bf16: the chunk's 8 elements; packed: the word holding its 8 bits
+    const int qcol = PK ? (hbit0 + 8 * qc) >> 5 : qc * 8;
+    qsh[m] = static_cast<uint32_t>((hbit0 + 8 * qc) & 31);
+    qoff[m] = in ? static_cast<uint32_t>((qn * a.q_row + qcol) * kElem) : kOutside;
+    koff[m] = in ? static_cast<uint32_t>((qn * a.k_row + qcol) * kElem) : kOutside;
     const int vp = c & 31, vn4 = c >> 5;
+    const int vcol = PK ? (hbit0 + 2 * vp) >> 5 : 2 * vp;
+    vsh[m] = static_cast<uint32_t>((hbit0 + 2 * vp) & 31);
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
       const int n = 4 * vn4 + x;
-      voff[m][x] = (2 * vp < a.d && n < a.N) ? static_cast<uint32_t>((n * a.v_row + 2 * vp) * 2) : kOutside;
+      voff[m][x] = (2 * vp < a.d && n < a.N) ? static_cast<uint32_t>((n * a.v_row + vcol) * kElem) : kOutside;
     }
   }
   u32x4 rq[2], rk[2];
   uint32_t rv[2][4];
   auto load_step = [&](int t) {
-    const __amdgpu_buffer_rsrc_t qr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(qb + t * a.q_t), 0, kRecords, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t kr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kb + t * a.k_t), 0, kRecords, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t vr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vb + t * a.v_t), 0, kRecords, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(reinterpret_cast<const unsigned char*>(qb) + t * a.q_t * kElem), 0, kRecords, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(reinterpret_cast<const unsigned char*>(kb) + t * a.k_t * kElem), 0, kRecords, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(reinterpret_cast<const unsigned char*>(vb) + t * a.v_t * kElem), 0, kRecords, kRsrcWord3);
+    if constexpr (PK) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        rq[m][0] = __builtin_amdgcn_raw_buffer_load_b32(qr, qoff[m], 0, 0);
+        rk[m][0] = __builtin_amdgcn_raw_buffer_load_b32(kr, koff[m], 0, 0);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) rv[m][x] = __builtin_amdgcn_raw_buffer_load_b32(vr, voff[m][x], 0, 0);
+      }
+      return;
+    }
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const i32x4 q4 = __builtin_amdgcn_raw_buffer_load_b128(qr, qoff[m], 0, 0);
@@ -172,6 +211,30 @@ __global__ __launch_bounds__(kThreads) void ssa_attention_kernel(AttnArgs a) {
     }
   };
   auto store_step = [&](int buf) {
+    if constexpr (PK) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int c = st + kStagers * m;
+        const int qn = c >> 3, qc = c & 7;
+        // the chunk's 8 dims sit at bit qsh of its word
+        *reinterpret_cast<u32x2*>(qs + buf * kStage + qn * kPitch + qc * 8) =
+            bits_to_bytes8(rq[m][0] >> qsh[m]);
+        *reinterpret_cast<u32x2*>(ks + buf * kStage + qn * kPitch + qc * 8) =
+            bits_to_bytes8(rk[m][0] >> qsh[m]);
+        // dims 2p, 2p+1 are bits vsh, vsh+1 of each token's word
+        const int vp = c & 31, vn4 = c >> 5;
+        const uint32_t sh = vsh[m];
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          w0 |= ((rv[m][x] >> sh) & 1u) << (8 * x);
+          w1 |= ((rv[m][x] >> (sh + 1)) & 1u) << (8 * x);
+        }
+        *reinterpret_cast<uint32_t*>(vt + buf * kStage + (2 * vp) * kPitch + 4 * vn4) = w0;
+        *reinterpret_cast<uint32_t*>(vt + buf * kStage + (2 * vp + 1) * kPitch + 4 * vn4) = w1;
+      }
+      return;
+    }
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const int c = st + kStagers * m;
@@ -252,6 +315,8 @@ __global__ __launch_bounds__(kThreads) void ssa_attention_kernel(AttnArgs a) {
         acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fv, fs, acc, 0, 0, 0);
       }
       uint16_t* ot = ob + t * a.o_t;
+      // packed: this lane's spikes at bit 8*e4 + 4*g + x of word od
+      uint32_t bits = 0;
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         uint32_t spk[4];
@@ -262,17 +327,25 @@ __global__ __launch_bounds__(kThreads) void ssa_attention_kernel(AttnArgs a) {
           const bool sp = hm >= a.vth;
           vm[e] = sp ? (SR ? __fsub_rn(hm, a.vth) : a.v_reset) : hm;
           spk[x] = sp ? 0x3F80u : 0u;
+          if constexpr (PK) bits |= (sp && od * 32 + 8 * e4 + 4 * g + x < a.d ? 1u : 0u) << (8 * e4 + 4 * g + x);
         }
-        // 4 dims from dd0; d % 8 == 0, so they are all in range when dd0 is
-        const int dd0 = od * 32 + 8 * e4 + 4 * g;
-        if (ti < a.N && dd0 < a.d) {
-          if (a.o_vec) {
-            *reinterpret_cast<u32x2*>(ot + dd0) = u32x2{spk[0] | (spk[1] << 16), spk[2] | (spk[3] << 16)};
-          } else {
+        if constexpr (!PK) {
+          // 4 dims from dd0; d % 8 == 0, so they are all in range when dd0 is
+          const int dd0 = od * 32 + 8 * e4 + 4 * g;
+          if (ti < a.N && dd0 < a.d) {
+            if (a.o_vec) {
+              *reinterpret_cast<u32x2*>(ot + dd0) = u32x2{spk[0] | (spk[1] << 16), spk[2] | (spk[3] << 16)};
+            } else {
 #pragma unroll
-            for (int x = 0; x < 4; ++x) ot[dd0 + x] = static_cast<uint16_t>(spk[x]);
+              for (int x = 0; x < 4; ++x) ot[dd0 + x] = static_cast<uint16_t>(spk[x]);
+            }
           }
         }
+      }
+      if constexpr (PK) {
+        // the two lane halves hold the word's other 16 bits (lane ^ 32)
+        bits |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(bits), 32));
+        if (g == 0 && ti < a.N && od * 32 < a.d) obw[t * a.o_t + od] = bits;
       }
       if (a.o_counts) {
         int32_t* oc = a.o_counts + ((static_cast<int64_t>(t) * a.B * a.H + bh) * a.N) * a.d;
@@ -287,6 +360,25 @@ __global__ __launch_bounds__(kThreads) void ssa_attention_kernel(AttnArgs a) {
     if (has_s && t + 1 < a.T) s_step(t + 1);
     __syncthreads();
   }
+}
+
+// Launch the core for args a (nt / dt: 32-token / 32-dim tiles).
+template <bool PK>
+int launch_core(const AttnArgs& a, int nt, int dt, bool soft, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(a.per_xcd) * 8u);
+  auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, a); };
+  if (soft) {
+    if (nt == 1 && dt == 1) launch(ssa_attention_kernel<1, 1, true, PK>);
+    else if (nt == 1) launch(ssa_attention_kernel<1, 2, true, PK>);
+    else if (dt == 1) launch(ssa_attention_kernel<2, 1, true, PK>);
+    else launch(ssa_attention_kernel<2, 2, true, PK>);
+  } else {
+    if (nt == 1 && dt == 1) launch(ssa_attention_kernel<1, 1, false, PK>);
+    else if (nt == 1) launch(ssa_attention_kernel<1, 2, false, PK>);
+    else if (dt == 1) launch(ssa_attention_kernel<2, 1, false, PK>);
+    else launch(ssa_attention_kernel<2, 2, false, PK>);
+  }
+  return launch_status();
 }
 
 }  // namespace
@@ -334,20 +426,51 @@ extern "C" int snnk_spike_attention(const uint16_t* q, const uint16_t* k, const 
   a.soft_reset = soft_reset ? 1 : 0;
   a.o_vec = aligned(spikes_out, 8) && out_row % 4 == 0 && out_step % 4 == 0;
   a.per_xcd = static_cast<int>((B * H + 7) / 8);
-  const dim3 grid(static_cast<unsigned>(a.per_xcd) * 8u);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int nt = N > 32 ? 2 : 1, dt = d > 32 ? 2 : 1;
-  auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, a); };
-  if (soft_reset) {
-    if (nt == 1 && dt == 1) launch(ssa_attention_kernel<1, 1, true>);
-    else if (nt == 1) launch(ssa_attention_kernel<1, 2, true>);
-    else if (dt == 1) launch(ssa_attention_kernel<2, 1, true>);
-    else launch(ssa_attention_kernel<2, 2, true>);
-  } else {
-    if (nt == 1 && dt == 1) launch(ssa_attention_kernel<1, 1, false>);
-    else if (nt == 1) launch(ssa_attention_kernel<1, 2, false>);
-    else if (dt == 1) launch(ssa_attention_kernel<2, 1, false>);
-    else launch(ssa_attention_kernel<2, 2, false>);
-  }
-  return launch_status();
+  return launch_core<false>(a, N > 32 ? 2 : 1, d > 32 ? 2 : 1, soft_reset != 0,
+                            static_cast<hipStream_t>(stream));
+}
+
+extern "C" int snnk_spike_attention_packed(const uint32_t* q, const uint32_t* k, const uint32_t* v,
+                                           int64_t q_row, int64_t k_row, int64_t v_row,
+                                           int64_t q_step, int64_t k_step, int64_t v_step,
+                                           int64_t in_head_bits, uint32_t* spikes_out,
+                                           int64_t out_row, int64_t out_step,
+                                           int64_t out_head_words,
+                                           int32_t* s_counts, int32_t* o_counts,
+                                           int64_t T, int64_t B, int64_t H, int64_t N, int64_t d,
+                                           float decay, float in_scale, float v_threshold,
+                                           float v_reset, int32_t soft_reset, void* stream) {
+  if (T < 0 || B < 0 || H <= 0 || N < 0 || d <= 0) return SNNK_EINVAL;
+  if (T == 0 || B == 0 || N == 0) return SNNK_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || spikes_out == nullptr) return SNNK_EINVAL;
+  if (d % 8 != 0 || N > kMaxTok || d > kMaxDim) return SNNK_EUNSUPPORTED;
+  if (in_head_bits < d || in_head_bits % 8 != 0 || out_head_words < (d + 31) / 32)
+    return SNNK_EINVAL;
+  if (!aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4) || !aligned(spikes_out, 4))
+    return SNNK_EALIGN;
+  const int64_t need_in = (H * in_head_bits + 31) / 32;
+  if (q_row < need_in || k_row < need_in || v_row < need_in || out_row < H * out_head_words)
+    return SNNK_EINVAL;
+  if (H * in_head_bits >= (int64_t{1} << 30)) return SNNK_EUNSUPPORTED;
+  if (B * H > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
+  // byte offsets of a step's token rows stay below 2^31 (buffer offsets)
+  if (std::max(q_row, std::max(k_row, v_row)) * kMaxTok * 4 >= (int64_t{1} << 31))
+    return SNNK_EUNSUPPORTED;
+  AttnArgs a{};
+  a.q = reinterpret_cast<const uint16_t*>(q);
+  a.k = reinterpret_cast<const uint16_t*>(k);
+  a.v = reinterpret_cast<const uint16_t*>(v);
+  a.q_row = q_row; a.k_row = k_row; a.v_row = v_row;
+  a.q_t = q_step; a.k_t = k_step; a.v_t = v_step;
+  a.out = reinterpret_cast<uint16_t*>(spikes_out); a.o_row = out_row; a.o_t = out_step;
+  a.s_counts = s_counts; a.o_counts = o_counts;
+  a.T = static_cast<int>(T); a.B = static_cast<int>(B); a.H = static_cast<int>(H);
+  a.N = static_cast<int>(N); a.d = static_cast<int>(d);
+  a.decay = decay; a.in_scale = in_scale; a.vth = v_threshold; a.v_reset = v_reset;
+  a.soft_reset = soft_reset ? 1 : 0;
+  a.hbits = static_cast<int>(in_head_bits);
+  a.ohw = static_cast<int>(out_head_words);
+  a.per_xcd = static_cast<int>((B * H + 7) / 8);
+  return launch_core<true>(a, N > 32 ? 2 : 1, d > 32 ? 2 : 1, soft_reset != 0,
+                           static_cast<hipStream_t>(stream));
 }

@@ -131,6 +131,9 @@ bool auto_cfg_packed(const ConvArgs& a, bool taps9, int* cfg, int* splits) {
   const bool pool = a.Ho != a.H;
   *splits = 1;
   if (!taps9) {                                   // Linear (FC, dense 2x2 maps)
+    // short-K projections over many rows (the SSA block's QKV: 8192 rows,
+    // K = 384, 1152 columns: 17.8 us with 128 x 64 tiles, 21.9 with 128 x 128)
+    if (rows >= 8192 && K <= 512) { *cfg = a.Cout > 512 ? 10 : 9; return true; }
     if (rows <= 64 || rows > 256) return false;
     if (K >= 4096) { *cfg = rows <= 128 ? 7 : 12; *splits = rows <= 128 ? 2 : 3; return true; }
     if (K >= 2048) { if (rows <= 128) return false; *cfg = 7; *splits = 2; return true; }
@@ -321,9 +324,12 @@ int run(const ConvArgs& a, bool pool, int tile_hint, int splits, bool allow_spli
   if (p.ws_bytes > 0 && (ws == nullptr || ws_bytes < p.ws_bytes)) return SNNK_EWORKSPACE;
   if (p.ws_bytes > 0 && !aligned(ws, 256)) return SNNK_EALIGN;
   if (packed_in || a.bits_out) {
-    // LIF variants only; the column-pooled Linear writes bf16 spikes
-    if (mean || a.pre != nullptr || (TAPS == 1 && pool && a.bits_out)) return SNNK_EUNSUPPORTED;
-    if (packed_in) return dispatch_packed(a, p, ws, s, pool, TAPS);
+    // LIF variants, and the pre-activation Linear on packed x; the
+    // column-pooled Linear writes bf16 spikes
+    const bool pre = a.pre != nullptr;
+    if (mean || (pre && (a.bits_out || TAPS != 1 || pool)) || (TAPS == 1 && pool && a.bits_out))
+      return SNNK_EUNSUPPORTED;
+    if (packed_in) return dispatch_packed(a, p, ws, s, pool, TAPS, pre);
   }
   if constexpr (TAPS == 1) {
     if (mean) return dispatch<false, MODE_MEAN, 1, false>(a, p, ws, s);
@@ -568,6 +574,24 @@ extern "C" int snnk_linear_bias_lif_act(const void* x, int32_t x_fmt, const uint
   st = apply_act_formats(&a, x, spikes_out, x_fmt, out_fmt, &packed_in);
   if (st != SNNK_OK) return st;
   return run<1>(a, col_pool != 0, tile_hint, splits, true, workspace, workspace_bytes,
+                static_cast<hipStream_t>(stream), false, packed_in);
+}
+
+extern "C" int snnk_linear_preact_act(const void* x, int32_t x_fmt, const uint16_t* w,
+                                      const float* bias, float* out, int64_t T, int64_t R,
+                                      int64_t K, int64_t N, int32_t tile_hint, int32_t splits,
+                                      void* workspace, int64_t workspace_bytes, void* stream) {
+  if (T == 0 || R == 0) return (T < 0 || R < 0) ? SNNK_EINVAL : SNNK_OK;
+  if (w == nullptr || !aligned(w, 16)) return w == nullptr ? SNNK_EINVAL : SNNK_EALIGN;
+  if (out == nullptr) return SNNK_EINVAL;
+  ConvArgs a;
+  int st = linear_args(static_cast<const uint16_t*>(x), w, bias, nullptr, out, T, R, K, N, 1.0f,
+                       1.0f, 1.0f, 0.0f, 0, false, &a, false);
+  if (st != SNNK_OK) return st;
+  bool packed_in = false;
+  st = apply_act_formats(&a, x, out, x_fmt, SNNK_ACT_BF16, &packed_in);
+  if (st != SNNK_OK) return st;
+  return run<1>(a, false, tile_hint, splits, true, workspace, workspace_bytes,
                 static_cast<hipStream_t>(stream), false, packed_in);
 }
 

@@ -857,10 +857,10 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
   }
 }
 
-// Packed-input LIF variants, instantiated in conv_packed.hip: the 3x3 conv
-// with or without the 2x2 pool (taps = 9) and the Linear with or without
-// the OR of column groups of four (taps = 1).
+// Packed-input variants, instantiated in conv_packed.hip: the 3x3 conv
+// with or without the 2x2 pool (taps = 9), the Linear with or without the
+// OR of column groups of four (taps = 1), and the pre-activation Linear.
 int dispatch_packed(const ConvArgs& a, const Plan& p, void* workspace, hipStream_t s, bool pool,
-                    int taps);
+                    int taps, bool preact);
 
 }  // namespace snnk

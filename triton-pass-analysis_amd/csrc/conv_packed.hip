@@ -8,7 +8,8 @@
 namespace snnk {
 
 int dispatch_packed(const ConvArgs& a, const Plan& p, void* workspace, hipStream_t s, bool pool,
-                    int taps) {
+                    int taps, bool preact) {
+  if (preact) return dispatch<false, MODE_PREACT, 1, true>(a, p, workspace, s);  // fp32 x.W^T + b
   if (taps == 1) {  // with pool: the OR of each group of four adjacent columns
     return pool ? dispatch<true, MODE_LIF, 1, true>(a, p, workspace, s)
                 : dispatch<false, MODE_LIF, 1, true>(a, p, workspace, s);

@@ -150,6 +150,25 @@ PROTOTYPES: dict[str, list] = {
         _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
         _i32, _p,              # soft_reset, stream
     ],
+    "snnk_spike_attention_packed": [
+        _p, _p, _p,            # q, k, v (uint32 words)
+        _i64, _i64, _i64,      # q_row, k_row, v_row (words)
+        _i64, _i64, _i64,      # q_step, k_step, v_step (words)
+        _i64,                  # in_head_bits
+        _p, _i64, _i64, _i64,  # spikes_out, out_row, out_step (words), out_head_words
+        _p, _p,                # s_counts, o_counts
+        _i64, _i64, _i64, _i64, _i64,  # T, B, H, N, d
+        _f32, _f32, _f32, _f32,  # decay, in_scale, v_threshold, v_reset
+        _i32, _p,              # soft_reset, stream
+    ],
+    "snnk_linear_preact_act": [
+        _p, _i32, _p, _p,      # x, x_fmt, w, bias
+        _p,                    # out (fp32)
+        _i64, _i64, _i64, _i64,  # T, R, K, N
+        _i32, _i32,            # tile_hint, splits
+        _p, _i64,              # workspace, workspace_bytes
+        _p,                    # stream
+    ],
     "snnk_spike_av_lif": [
         _p, _i32, _p, _i32,    # q, q_dtype, kv, kv_dtype
         _p,                    # spikes_out

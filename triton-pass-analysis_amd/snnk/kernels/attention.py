@@ -20,7 +20,7 @@ import torch
 
 from .. import _abi
 from .binary import pack_bits, _gemm_packed
-from .linear import linear_bias_lif, linear_preact
+from .linear import linear_bias_lif_act, linear_preact_act, linear_bias_lif, linear_preact
 from .neurons import if_lif, launch_lif, THR_SCALAR
 
 # popcount is native on gfx950 (v_bcnt_u32_b32); kept for API parity with
@@ -158,6 +158,67 @@ def spike_attention(q, k, v, *, B: int, N: int, heads: int, scale: float, tau: f
     return (out, S, O) if return_counts else out
 
 
+def spike_attention_packed(q, k, v, *, B: int, N: int, heads: int, d: int, in_head_bits: int,
+                           out_head_words: int, scale: float, tau: float = 2.0,
+                           decay: float | None = None, decay_input: bool = True,
+                           v_threshold: float = 0.5, v_reset: float = 0.0,
+                           soft_reset: bool = False, out: torch.Tensor | None = None,
+                           return_counts: bool = False):
+    """:func:`spike_attention` on packed spikes.
+
+    q, k, v: int32 words ``[T, B*N, W]`` (any row stride, e.g. column slices
+    of one packed QKV projection output); head h starts at bit
+    ``h*in_head_bits`` of a row (LSB first; ``in_head_bits = d`` for the rows
+    a packed projection writes).  Returns packed spikes
+    ``[T, B*N, heads*out_head_words]``, head h on words ``h*out_head_words ..``
+    with its bits past d zero (and with ``return_counts`` the int32 S and O).
+    N <= 64, d <= 64, d % 8 == 0.
+    """
+    for t in (q, k, v):
+        assert t.is_cuda and t.dtype == torch.int32 and t.ndim == 3 and t.stride(2) == 1
+    T, R, _ = q.shape
+    assert R == B * N and k.shape[:2] == q.shape[:2] and v.shape[:2] == q.shape[:2]
+    dec, in_scale = _lif_scale(tau, decay, decay_input, scale)
+    if out is None:
+        out = torch.empty(T, R, heads * out_head_words, device=q.device, dtype=torch.int32)
+    S = O = None
+    if return_counts:
+        S = torch.empty(T, B, heads, N, N, device=q.device, dtype=torch.int32)
+        O = torch.empty(T, B, heads, N, d, device=q.device, dtype=torch.int32)
+    with torch.cuda.device(q.device):
+        _abi.call("snnk_spike_attention_packed", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                  q.stride(1), k.stride(1), v.stride(1), q.stride(0), k.stride(0), v.stride(0),
+                  in_head_bits, out.data_ptr(), out.stride(1), out.stride(0), out_head_words,
+                  _abi.ptr(S), _abi.ptr(O), T, B, heads, N, d, float(dec), float(in_scale),
+                  float(v_threshold), float(v_reset), 1 if soft_reset else 0,
+                  _abi.stream(q.device))
+    return (out, S, O) if return_counts else out
+
+
+def pad_heads_rows(w: torch.Tensor, b: torch.Tensor | None, heads: int, slot: int):
+    """Rows of a [heads*d, K] projection (and its bias) spread to ``slot`` rows
+    per head, the rows past d zero: its spikes come out with every head
+    starting on a 32-bit word of a packed row (and never firing past d)."""
+    d = w.shape[0] // heads
+    wp = torch.zeros(heads, slot, w.shape[1], device=w.device, dtype=w.dtype)
+    wp[:, :d] = w.view(heads, d, -1)
+    bp = None
+    if b is not None:
+        bp = torch.zeros(heads, slot, device=b.device, dtype=b.dtype)
+        bp[:, :d] = b.view(heads, d)
+        bp = bp.reshape(-1).contiguous()
+    return wp.reshape(heads * slot, -1).contiguous(), bp
+
+
+def pad_heads_cols(w: torch.Tensor, heads: int, slot: int) -> torch.Tensor:
+    """Columns of a [N, heads*d] projection spread to ``slot`` columns per
+    head (zeros past d), to read head-padded packed spikes."""
+    d = w.shape[1] // heads
+    wp = torch.zeros(w.shape[0], heads, slot, device=w.device, dtype=w.dtype)
+    wp[:, :, :d] = w.view(w.shape[0], heads, d)
+    return wp.reshape(w.shape[0], heads * slot).contiguous()
+
+
 def spike_self_attention(tokens, w_qkv, b_qkv, w_proj, b_proj, *, heads: int,
                          scale: float = 0.125, tau: float = 2.0, vth_qkv: float = 1.0,
                          vth_attn: float = 0.5, input_vth: float | None = None,
@@ -184,6 +245,52 @@ def spike_self_attention(tokens, w_qkv, b_qkv, w_proj, b_proj, *, heads: int,
                           v_threshold=vth_attn, return_counts=return_intermediates)
     attn = res[0] if return_intermediates else res
     out = linear_preact(attn, w_proj, b_proj).view(T, B, N, D)
+    if return_intermediates:
+        return out, dict(qkv=qkv, attn=attn, S=res[1], O=res[2])
+    return out
+
+
+def prepare_ssa_packed(w_qkv, b_qkv, w_proj, *, heads: int) -> dict:
+    """Weights of :func:`spike_self_attention` laid out for the packed block:
+    the QKV projection as is (its packed output holds the heads back to back,
+    ``d`` bits each), the output projection's input columns padded to whole
+    32-bit words per head, the layout in which the packed attention core
+    writes its spikes.  Built once per set of weights."""
+    D = w_proj.shape[0]
+    assert w_qkv.shape == (3 * D, D) and D % heads == 0 and D % 32 == 0
+    d = D // heads
+    slot = 32 * ((d + 31) // 32)
+    return dict(w_qkv=w_qkv.to(torch.bfloat16).contiguous(),
+                b_qkv=None if b_qkv is None else b_qkv.float().contiguous(),
+                w_proj=pad_heads_cols(w_proj, heads, slot).to(torch.bfloat16).contiguous(),
+                heads=heads, d=d, slot=slot, D=D)
+
+
+def spike_self_attention_packed(x_words, prep: dict, b_proj, *, B: int, N: int,
+                                scale: float = 0.125, tau: float = 2.0, vth_qkv: float = 1.0,
+                                vth_attn: float = 0.5, return_intermediates: bool = False):
+    """:func:`spike_self_attention` with the spikes packed end to end.
+
+    x_words: int32 ``[T, B*N, D // 32]`` packed input spikes (bit c%32 of word
+    c//32, as the LIF kernel writes them); ``prep`` from
+    :func:`prepare_ssa_packed`.  Q, K and V leave the projection as packed
+    words ``[T, B*N, 3D // 32]``, the attention core reads them and writes its
+    spikes with every head on whole words, and the output projection reads
+    those: output fp32 ``[T, B, N, D]``, the same spikes (and the output up to
+    fp32 summation order) as the bf16 block.
+    """
+    T = x_words.shape[0]
+    H, hw, D, d = prep["heads"], prep["slot"] // 32, prep["D"], prep["d"]
+    dec = 1.0 - 1.0 / tau
+    qkv = linear_bias_lif_act(x_words, prep["w_qkv"], prep["b_qkv"], decay=dec,
+                              in_scale=1.0 / tau, v_threshold=vth_qkv, out_bits=True)
+    Dw = D // 32
+    q, k, v = qkv[..., :Dw], qkv[..., Dw:2 * Dw], qkv[..., 2 * Dw:]
+    res = spike_attention_packed(q, k, v, B=B, N=N, heads=H, d=d, in_head_bits=d,
+                                 out_head_words=hw, scale=scale, tau=tau, v_threshold=vth_attn,
+                                 return_counts=return_intermediates)
+    attn = res[0] if return_intermediates else res
+    out = linear_preact_act(attn, prep["w_proj"], b_proj).view(T, B, N, D)
     if return_intermediates:
         return out, dict(qkv=qkv, attn=attn, S=res[1], O=res[2])
     return out

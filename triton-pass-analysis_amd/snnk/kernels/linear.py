@@ -152,6 +152,38 @@ def linear_preact(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *
     return out
 
 
+def linear_preact_act(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
+                      out: torch.Tensor | None = None, tile_hint: int = -1,
+                      splits: int | None = None) -> torch.Tensor:
+    """:func:`linear_preact` on bf16 ``[T, R, K]`` or int32 packed ``[T, R, K // 32]``
+    spike rows: fp32 ``x.w^T + bias`` ``[T, R, N]`` (no neuron)."""
+    assert x.is_cuda and x.ndim == 3 and x.is_contiguous()
+    if x.dtype == torch.int32:
+        x_fmt, K = _abi.ACT_BITS, x.shape[2] * 32
+    else:
+        assert x.dtype == torch.bfloat16, x.dtype
+        x_fmt, K = _abi.ACT_BF16, x.shape[2]
+    T, R = x.shape[:2]
+    N = w.shape[0]
+    assert w.dtype == torch.bfloat16 and w.shape == (N, K) and w.is_contiguous() \
+        and w.device == x.device
+    if bias is not None:
+        assert bias.dtype == torch.float32 and bias.numel() == N and bias.is_contiguous()
+    if out is None:
+        out = torch.empty(T, R, N, device=x.device, dtype=torch.float32)
+    else:
+        assert out.shape == (T, R, N) and out.dtype == torch.float32 and out.is_contiguous()
+    sp = 0 if splits is None else int(splits)
+    with torch.cuda.device(x.device):
+        nbytes = _abi.size_call("snnk_linear_bias_lif_act_ws_size", T, R, K, N, x_fmt, 0,
+                                int(tile_hint), sp)
+        ws = _workspace.get(x.device, nbytes)
+        _abi.call("snnk_linear_preact_act", x.data_ptr(), x_fmt, w.data_ptr(), _abi.ptr(bias),
+                  out.data_ptr(), T, R, K, N, int(tile_hint), sp, _abi.ptr(ws),
+                  0 if ws is None else ws.numel(), _abi.stream(x.device))
+    return out
+
+
 def linear_mean_t(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
                   out: torch.Tensor | None = None, tile_hint: int = -1,
                   splits: int | None = None) -> torch.Tensor:
