@@ -132,6 +132,10 @@ static_assert(offsetof(ConvArgs, x) / 64 == 0 && offsetof(ConvArgs, div_cin) / 6
                   sizeof(ConvArgs) <= 256,
               "the kernel touches one field per 64-byte line of ConvArgs");
 
+// LDS of a resident-weight block (NBUF = 0): every K stage of its BN weight
+// rows, 128 bytes per row and stage.
+constexpr int kResBytes = 160 * 1024;
+
 template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool PK = false>
 struct Cfg {
   static constexpr int kWaves = WM * WN * KSPLIT;
@@ -139,6 +143,13 @@ struct Cfg {
   static constexpr int BM = WM * TM * 32;
   static constexpr int BN = WN * TN * 32;
   static constexpr int kQuads = BM / 16;                    // quads per block
+  // NBUF = 0: resident weights.  The block's BN weight rows stay in LDS for
+  // all K (loaded once), and each lane loads the packed spike words of its
+  // own A rows straight into registers a few stages ahead: the K loop has no
+  // barrier and no LDS ring.  Packed A only, one K group, K % 64 == 0 and
+  // K * BN * 2 <= kResBytes.
+  static constexpr bool kRes = NBUF == 0;
+  static_assert(!kRes || (PK && KSPLIT == 1), "resident weights: packed A, one K group");
   // operand stages arrive by direct-to-LDS loads; the WM*WN waves of a K
   // group share them.  B (and bf16 A): 16 bytes per lane, one wave-wide load
   // filling kDmaRows rows (1 KB).  Packed A (PK): the stage's 64 bits of a
@@ -148,21 +159,24 @@ struct Cfg {
   static constexpr int kSegA = BM / kARowsPerSeg;
   static constexpr int kSegB = BN / kDmaRows;
   static constexpr int kGroupWaves = WM * WN;
-  static_assert((PK || kSegA % kGroupWaves == 0) && kSegB % kGroupWaves == 0,
+  static_assert(kRes || ((PK || kSegA % kGroupWaves == 0) && kSegB % kGroupWaves == 0),
                 "segments must split evenly over a group's waves");
   // per wave: A segments first, then B segments.  Packed A segments may not
   // split evenly: the spare waves load a segment again (same bytes to the
-  // same place), so that every wave issues the same number of loads
-  static constexpr int kAPer = (kSegA + kGroupWaves - 1) / kGroupWaves;
-  static constexpr int kBPer = kSegB / kGroupWaves;
+  // same place), so that every wave issues the same number of loads.
+  // Resident weights: the TM rows of the lane's accumulator tiles.
+  static constexpr int kAPer = kRes ? TM : (kSegA + kGroupWaves - 1) / kGroupWaves;
+  static constexpr int kBPer = kRes ? 0 : kSegB / kGroupWaves;
   static constexpr int kSegPer = kAPer + kBPer;
   static constexpr int kAStageBytes = KSPLIT * BM * kARowBytes;  // B follows A in a stage
   static constexpr int kStageBytes = kAStageBytes + KSPLIT * BN * kRowBytes;
   static constexpr int kBuf = NBUF;  // ring of operand stages in LDS
-  static constexpr int kLdsBytes = kBuf * kStageBytes;
+  static constexpr int kLdsBytes = kRes ? kResBytes : kBuf * kStageBytes;
   static constexpr int kRedBytes = (KSPLIT - 1) * WM * WN * TM * TN * 16 * 64 * 4;
   static constexpr int kSmem = kLdsBytes > kRedBytes ? kLdsBytes : kRedBytes;
-  static_assert(NBUF >= 2 && kSmem <= 160 * 1024, "LDS ring must fit 160 KB");
+  static_assert((kRes || NBUF >= 2) && kSmem <= 160 * 1024, "LDS ring must fit 160 KB");
+  // K stages of the resident weights that fit
+  static constexpr int kResStages = kResBytes / (BN * kRowBytes);
 };
 
 __device__ __forceinline__ uint16_t spike_bf16(bool s) { return s ? 0x3F80u : 0u; }
@@ -280,9 +294,11 @@ void conv3x3_kernel(ConvArgs a) {
 #pragma unroll
   for (int i = 0; i < C::kSegPer; ++i) {
     if (i < C::kAPer) {
-      // packed A: lane l takes row 32*q + l/2, half l%2 (its 4 bytes)
+      // packed A: lane l takes row 32*q + l/2, half l%2 (its 4 bytes);
+      // resident weights: row l%32 of the wave's accumulator tile i
       const int q = PK ? (wmn + i * C::kGroupWaves) % C::kSegA : wmn + i * C::kGroupWaves;
-      const int r = PK ? 32 * q + (lane >> 1) : kDmaRows * q + lrow;
+      const int r = C::kRes ? (wm * TM + i) * 32 + (lane & 31)
+                            : PK ? 32 * q + (lane >> 1) : kDmaRows * q + lrow;
       const int rr = r & 31;
       const int pq = rr >> 3, gr = (rr >> 2) & 1, t = rr & 3;
       const int quad = quad0 + (r >> 5) * 2 + gr;
@@ -500,105 +516,90 @@ void conv3x3_kernel(ConvArgs a) {
     }
   };
 
-  for (int tc = 0; tc < n_chunks; ++tc) {
-    // Source offsets of this lane's A segments for the tap pair (tap_lo,
-    // tap_hi) of the stage last prepared: kFar where the row, the step or
-    // the tap's source pixel does not exist.  A stage then costs one add
-    // per segment; the offsets are rebuilt only when the tap pair changes.
-    // (the step of this lane's A rows: row & 3, with row 8*q + l/8 -- or
-    // 32*q + l/2 for packed A)
-    const bool t_ok = tc * 4 + ((PK ? lane >> 1 : lrow) & 3) < a.T;
-    const uint32_t chunk_off = static_cast<uint32_t>(tc) * 4u * a.x_tstride_b;
-    uint32_t a_off[C::kAPer];
-#pragma unroll
-    for (int i = 0; i < C::kAPer; ++i) a_off[i] = kFar;
-    int cur_lo = -1, cur_hi = -1;
-
-    // wave-uniform addressing of group-local stage sl
-    struct StageAddr {
-      bool live;        // a stage of the ring loop (later slots are not loaded)
-      bool zero_b;      // B reads zeros: a stage past the block's K range
-      bool tail;        // the last stage of K % 64 == 32: upper half past K
-      uint32_t da, db;  // A: chunk + channel bytes of the lower half; B: bytes of k0
-    };
-    auto prepare = [&](int sl) {
-      StageAddr p;
-      const int sg = st_begin + sl * KSPLIT + kg;
-      p.live = sl < n_stages_g;
-      p.zero_b = sg >= st_end;
-      const uint32_t k0 = p.zero_b ? 0u : static_cast<uint32_t>(sg * kKS);
-      const int tap_lo = static_cast<int>(fdiv(k0, a.div_cin));
-      const int cin_lo = static_cast<int>(k0) - tap_lo * a.Cin;
-      const bool wrap = cin_lo + 32 >= a.Cin;  // upper half starts the next tap
-      const int tap_hi = tap_lo + (wrap ? 1 : 0);
-      p.da = chunk_off + static_cast<uint32_t>(cin_lo) * 2u;
-      p.db = k0 * 2u;
-      p.tail = static_cast<int>(k0) + 32 >= K;
-      if (p.live && p.zero_b) {  // (rare) every A offset past the end as well
-        cur_lo = cur_hi = -1;
-        p.da = 0;
-#pragma unroll
-        for (int i = 0; i < C::kAPer; ++i) a_off[i] = kFar;
-      } else if (p.live && (tap_lo != cur_lo || tap_hi != cur_hi)) {
-        cur_lo = tap_lo;
-        cur_hi = tap_hi;
-        // byte delta of each half's source pixel, relative to p.da; the upper
-        // half sits 32 channels on, or at channel cin_lo + 32 - Cin of the
-        // next tap (a tap past the last has no ok bit: zeros)
-        const int32_t del_lo = (tap_dy<TAPS>(tap_lo) * a.W + tap_dx<TAPS>(tap_lo)) * a.Cin * 2;
-        const int32_t del_hi = (tap_dy<TAPS>(tap_hi) * a.W + tap_dx<TAPS>(tap_hi)) * a.Cin * 2 +
-                               64 - (wrap ? 2 * a.Cin : 0);
-#pragma unroll
-        for (int i = 0; i < C::kAPer; ++i) {
-          const uint32_t h = PK ? static_cast<uint32_t>(lane & 1)
-                                : h0 ^ static_cast<uint32_t>((wmn + i * C::kGroupWaves) & 1);
-          const int tap = h ? tap_hi : tap_lo;
-          const bool ok = t_ok && ((s_ok[i] >> tap) & 1u);
-          a_off[i] = ok ? s_base[i] + static_cast<uint32_t>(h ? del_hi : del_lo) : kFar;
-        }
-      }
-      return p;
-    };
-    // enqueue the direct global->LDS load of segment i of a stage.  A ring
-    // slot past the loop is loaded too (never read; its offsets stay inside
-    // the operands or read zeros): a branch around each load cost more than
-    // the loads, and the waits stay conservative
-    auto issue_seg = [&](const StageAddr& p, int i, int buf) {
-      unsigned char* stage = smem + buf * C::kStageBytes;
-      if (i < C::kAPer) {  // resolved at compile time
-        // (the offset goes through a variable: with the sum written in the
-        // call, hipcc's host pass drops the kernel's launch stub)
-        const uint32_t off = a_off[i] + p.da;
-        if constexpr (PK) {
-          // packed x: the 32 spikes of this lane's half-row are 4 bytes at a
-          // sixteenth of the bf16 offset (past-the-end offsets stay past it)
-          const int q = (wmn + i * C::kGroupWaves) % C::kSegA;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              xr, (lds_ptr_t)(stage + kg * C::BM * 8 + q * 256), 4, off >> 4, 0, 0, 0);
-        } else {
-          const int q = wmn + i * C::kGroupWaves;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              xr, (lds_ptr_t)(stage + (kg * C::BM + kDmaRows * q) * kRowBytes), 16, off, 0, 0, 0);
-        }
-      } else {
-        const int q = wmn + (i - C::kAPer) * C::kGroupWaves;
-        const bool upper = (h0 ^ static_cast<uint32_t>(q & 1)) != 0;
-        const uint32_t off = (p.zero_b || (p.tail && upper)) ? kFar : s_base[i] + p.db;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            wr, (lds_ptr_t)(stage + C::kAStageBytes + (kg * C::BN + kDmaRows * q) * kRowBytes),
-            16, off, 0, 0, 0);
-      }
-    };
-
-    // a loop, not unrolled: this code runs once per launch from a cold
-    // instruction cache, so one copy of it is fetched instead of NBUF-1
-#pragma nounroll
-    for (int p = 0; p < C::kBuf - 1; ++p) {
-      const StageAddr sp = prepare(p);
-#pragma unroll
-      for (int i = 0; i < C::kSegPer; ++i) issue_seg(sp, i, p);
+  // ---- resident weights: one fill, then K loops without barriers ----------
+  if constexpr (C::kRes) {
+    // fill segment g: weight rows 8*(g % kSegB).. of K stage g / kSegB, one
+    // 16-byte chunk per lane, swizzled as in the ring; LDS stage s holds the
+    // block's BN rows at 128 bytes each
+    const int n_seg = a.n_stages * C::kSegB;
+    for (int g = wave; g < n_seg; g += C::kWaves) {
+      const int st = g / C::kSegB;
+      const int n = 8 * (g - st * C::kSegB) + lrow;
+      const uint32_t off = n0 + n < a.Cout
+                               ? static_cast<uint32_t>(n0 + n) * static_cast<uint32_t>(K) * 2u +
+                                     static_cast<uint32_t>(st) * kRowBytes + swz(n, slot) * 16u
+                               : kFar;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          wr, (lds_ptr_t)(smem + (st * C::BN + n - lrow) * kRowBytes), 16, off, 0, 0, 0);
     }
-    // set-up that no load waits for
+  }
+  // A rows with resident weights: the 64 spikes of stage s of the lane's row
+  // (wm*TM + i)*32 + lane%32 are 8 bytes of packed words, loaded into
+  // registers kAhead stages before their MFMAs.  The stage loop is unrolled
+  // by kAhead so that each stage has registers of its own (a rotation would
+  // wait for every load in flight).
+  constexpr int kAhead = 3;
+  auto res_k_loop = [&](f32x16 (&acc)[TM][TN], int tc, bool t_ok, uint32_t chunk_off)
+                        __attribute__((always_inline)) {
+    const int n_st = a.n_stages;
+    uint32_t a_off[TM];
+    int cur_tap = -1;
+    auto load_a = [&](int s, u32x2 (&dst)[TM]) __attribute__((always_inline)) {
+      const uint32_t k0 = static_cast<uint32_t>(s) * kKS;
+      const int tap = static_cast<int>(fdiv(k0, a.div_cin));
+      const int cin_lo = static_cast<int>(k0) - tap * a.Cin;
+      if (tap != cur_tap) {  // every Cin / 64 stages
+        cur_tap = tap;
+        const int32_t del = (tap_dy<TAPS>(tap) * a.W + tap_dx<TAPS>(tap)) * a.Cin * 2;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          a_off[i] = t_ok && ((s_ok[i] >> tap) & 1u) ? s_base[i] + static_cast<uint32_t>(del) : kFar;
+      }
+      const uint32_t da = chunk_off + static_cast<uint32_t>(cin_lo) * 2u;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)  // packed byte offset: a sixteenth of the bf16 one
+        dst[i] = __builtin_amdgcn_raw_buffer_load_b64(xr, static_cast<int>((a_off[i] + da) >> 4), 0, 0);
+    };
+    auto stage = [&](int s, u32x2 (&pa)[TM]) __attribute__((always_inline)) {
+      // expand the four k-slices first; the registers then take stage s + kAhead
+      bf16x8 fa[4][TM];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const u32x4 e = bits_to_bf16x8((pa[i][kk >> 1] >> (16 * (kk & 1) + 8 * g_lane)) & 0xFFu);
+          __builtin_memcpy(&fa[kk][i], &e, 16);
+        }
+      if (s + kAhead < n_st) load_a(s + kAhead, pa);
+      const uint16_t* sb =
+          reinterpret_cast<const uint16_t*>(smem) + (s * C::BN + wn * TN * 32 + r_lane) * kRow;
+      bf16x8 fb[2][TN];
+      auto read_b = [&](bf16x8 (&dst)[TN], int kk) __attribute__((always_inline)) {
+        const int ch = swz(r_lane, kk * 2 + g_lane) * 8;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) dst[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRow + ch);
+      };
+      read_b(fb[0], 0);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        if (kk + 1 < 4) read_b(fb[(kk + 1) & 1], kk + 1);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    u32x2 ring[kAhead][TM];
+#pragma unroll
+    for (int d = 0; d < kAhead; ++d)
+      if (d < n_st) load_a(d, ring[d]);
     if (tc == 0) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
@@ -606,77 +607,196 @@ void conv3x3_kernel(ConvArgs a) {
         col_ok[j] = n < a.Cout;
         bias_n[j] = (a.bias && col_ok[j]) ? a.bias[n] : 0.0f;
       }
+      wait_vmcnt_barrier<0>();  // the resident weights are in LDS
     }
-    f32x16 acc[TM][TN];
+    for (int s0 = 0; s0 < n_st; s0 += kAhead) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-    constexpr int kSlices = kKS / 16;
-    int buf = 0;
-    // addressing of the stage the next iteration loads; prepared at the end
-    // of the previous iteration, so that after each barrier the fragment
-    // reads issue at once instead of behind the scalar stage arithmetic
-    StageAddr sp = prepare(C::kBuf - 1);
-    for (int s = 0; s < n_stages_g; ++s) {
-      // this wave's loads of stage s are done once at most the later
-      // stages' loads are outstanding; the barrier publishes every wave's
-      // loads and retires the reads of the buffer refilled next
-      wait_stages_barrier<C::kSegPer, C::kBuf - 2>(n_stages_g - 1 - s);
-      const int nbuf = buf == 0 ? C::kBuf - 1 : buf - 1;
+      for (int d = 0; d < kAhead; ++d)
+        if (s0 + d < n_st) stage(s0 + d, ring[d]);
+    }
+  };
 
-      const unsigned char* st = smem + buf * C::kStageBytes;
-      const uint16_t* sa = reinterpret_cast<const uint16_t*>(st) + (kg * C::BM + wm * TM * 32 + r_lane) * kRow;
-      const uint16_t* sb = reinterpret_cast<const uint16_t*>(st + C::kAStageBytes) +
-                           (kg * C::BN + wn * TN * 32 + r_lane) * kRow;
-      // packed A: the stage's 64 bits of each of this lane's rows; slice kk,
-      // half g reads byte 2*kk + g (K values 16*kk + 8*g ..)
-      u32x2 pa[TM];
-      if constexpr (PK) {
+  for (int tc = 0; tc < n_chunks; ++tc) {
+    // Source offsets of this lane's A segments for the tap pair (tap_lo,
+    // tap_hi) of the stage last prepared: kFar where the row, the step or
+    // the tap's source pixel does not exist.  A stage then costs one add
+    // per segment; the offsets are rebuilt only when the tap pair changes.
+    // (the step of this lane's A rows: row & 3, with row 8*q + l/8 -- or
+    // 32*q + l/2 for packed A, or lane%32 with resident weights)
+    const bool t_ok = tc * 4 + ((C::kRes ? lane : PK ? lane >> 1 : lrow) & 3) < a.T;
+    const uint32_t chunk_off = static_cast<uint32_t>(tc) * 4u * a.x_tstride_b;
+    f32x16 acc[TM][TN];
+    if constexpr (C::kRes) {
+      res_k_loop(acc, tc, t_ok, chunk_off);
+    } else {
+      uint32_t a_off[C::kAPer];
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          pa[i] = *reinterpret_cast<const u32x2*>(st + (kg * C::BM + wm * TM * 32 + i * 32 + r_lane) * 8);
-      }
-      auto read = [&](bf16x8 (&fa)[TM], bf16x8 (&fb)[TN], int kk) {
-        // tile rows start at multiples of 32, so the swizzle depends on r_lane only
-        const int ch = swz(r_lane, kk * 2 + g_lane) * 8;
+      for (int i = 0; i < C::kAPer; ++i) a_off[i] = kFar;
+      int cur_lo = -1, cur_hi = -1;
+
+      // wave-uniform addressing of group-local stage sl
+      struct StageAddr {
+        bool live;        // a stage of the ring loop (later slots are not loaded)
+        bool zero_b;      // B reads zeros: a stage past the block's K range
+        bool tail;        // the last stage of K % 64 == 32: upper half past K
+        uint32_t da, db;  // A: chunk + channel bytes of the lower half; B: bytes of k0
+      };
+      auto prepare = [&](int sl) {
+        StageAddr p;
+        const int sg = st_begin + sl * KSPLIT + kg;
+        p.live = sl < n_stages_g;
+        p.zero_b = sg >= st_end;
+        const uint32_t k0 = p.zero_b ? 0u : static_cast<uint32_t>(sg * kKS);
+        const int tap_lo = static_cast<int>(fdiv(k0, a.div_cin));
+        const int cin_lo = static_cast<int>(k0) - tap_lo * a.Cin;
+        const bool wrap = cin_lo + 32 >= a.Cin;  // upper half starts the next tap
+        const int tap_hi = tap_lo + (wrap ? 1 : 0);
+        p.da = chunk_off + static_cast<uint32_t>(cin_lo) * 2u;
+        p.db = k0 * 2u;
+        p.tail = static_cast<int>(k0) + 32 >= K;
+        if (p.live && p.zero_b) {  // (rare) every A offset past the end as well
+          cur_lo = cur_hi = -1;
+          p.da = 0;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          if constexpr (PK) {
-            const u32x4 e = bits_to_bf16x8((pa[i][kk >> 1] >> (16 * (kk & 1) + 8 * g_lane)) & 0xFFu);
-            __builtin_memcpy(&fa[i], &e, 16);
-          } else {
-            fa[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kRow + ch);
+          for (int i = 0; i < C::kAPer; ++i) a_off[i] = kFar;
+        } else if (p.live && (tap_lo != cur_lo || tap_hi != cur_hi)) {
+          cur_lo = tap_lo;
+          cur_hi = tap_hi;
+          // byte delta of each half's source pixel, relative to p.da; the upper
+          // half sits 32 channels on, or at channel cin_lo + 32 - Cin of the
+          // next tap (a tap past the last has no ok bit: zeros)
+          const int32_t del_lo = (tap_dy<TAPS>(tap_lo) * a.W + tap_dx<TAPS>(tap_lo)) * a.Cin * 2;
+          const int32_t del_hi = (tap_dy<TAPS>(tap_hi) * a.W + tap_dx<TAPS>(tap_hi)) * a.Cin * 2 +
+                                 64 - (wrap ? 2 * a.Cin : 0);
+#pragma unroll
+          for (int i = 0; i < C::kAPer; ++i) {
+            const uint32_t h = PK ? static_cast<uint32_t>(lane & 1)
+                                  : h0 ^ static_cast<uint32_t>((wmn + i * C::kGroupWaves) & 1);
+            const int tap = h ? tap_hi : tap_lo;
+            const bool ok = t_ok && ((s_ok[i] >> tap) & 1u);
+            a_off[i] = ok ? s_base[i] + static_cast<uint32_t>(h ? del_hi : del_lo) : kFar;
           }
         }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRow + ch);
+        return p;
       };
-      // software pipeline over the k-slices: the reads of slice kk+1 and a
-      // share of the next stage's loads are in flight while slice kk's MFMAs
-      // run (the compiler's own interleaving measured 3-6% faster than
-      // scheduling barriers around each MFMA group)
-      bf16x8 fa[2][TM], fb[2][TN];
-      read(fa[0], fb[0], 0);
+      // enqueue the direct global->LDS load of segment i of a stage.  A ring
+      // slot past the loop is loaded too (never read; its offsets stay inside
+      // the operands or read zeros): a branch around each load cost more than
+      // the loads, and the waits stay conservative
+      auto issue_seg = [&](const StageAddr& p, int i, int buf) {
+        unsigned char* stage = smem + buf * C::kStageBytes;
+        if (i < C::kAPer) {  // resolved at compile time
+          // (the offset goes through a variable: with the sum written in the
+          // call, hipcc's host pass drops the kernel's launch stub)
+          const uint32_t off = a_off[i] + p.da;
+          if constexpr (PK) {
+            // packed x: the 32 spikes of this lane's half-row are 4 bytes at a
+            // sixteenth of the bf16 offset (past-the-end offsets stay past it)
+            const int q = (wmn + i * C::kGroupWaves) % C::kSegA;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (lds_ptr_t)(stage + kg * C::BM * 8 + q * 256), 4, off >> 4, 0, 0, 0);
+          } else {
+            const int q = wmn + i * C::kGroupWaves;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (lds_ptr_t)(stage + (kg * C::BM + kDmaRows * q) * kRowBytes), 16, off, 0, 0, 0);
+          }
+        } else {
+          const int q = wmn + (i - C::kAPer) * C::kGroupWaves;
+          const bool upper = (h0 ^ static_cast<uint32_t>(q & 1)) != 0;
+          const uint32_t off = (p.zero_b || (p.tail && upper)) ? kFar : s_base[i] + p.db;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              wr, (lds_ptr_t)(stage + C::kAStageBytes + (kg * C::BN + kDmaRows * q) * kRowBytes),
+              16, off, 0, 0, 0);
+        }
+      };
+
+      // a loop, not unrolled: this code runs once per launch from a cold
+      // instruction cache, so one copy of it is fetched instead of NBUF-1
+#pragma nounroll
+      for (int p = 0; p < C::kBuf - 1; ++p) {
+        const StageAddr sp = prepare(p);
 #pragma unroll
-      for (int kk = 0; kk < kSlices; ++kk) {
-        if (kk + 1 < kSlices) read(fa[(kk + 1) & 1], fb[(kk + 1) & 1], kk + 1);
-#pragma unroll
-        for (int i = 0; i < C::kSegPer; ++i)
-          if (i % kSlices == kk) issue_seg(sp, i, nbuf);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < C::kSegPer; ++i) issue_seg(sp, i, p);
       }
-      sp = prepare(s + C::kBuf);
-      buf = buf + 1 == C::kBuf ? 0 : buf + 1;
+      // set-up that no load waits for
+      if (tc == 0) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = n0 + (wn * TN + j) * 32 + r_lane;
+          col_ok[j] = n < a.Cout;
+          bias_n[j] = (a.bias && col_ok[j]) ? a.bias[n] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+      constexpr int kSlices = kKS / 16;
+      int buf = 0;
+      // addressing of the stage the next iteration loads; prepared at the end
+      // of the previous iteration, so that after each barrier the fragment
+      // reads issue at once instead of behind the scalar stage arithmetic
+      StageAddr sp = prepare(C::kBuf - 1);
+      for (int s = 0; s < n_stages_g; ++s) {
+        // this wave's loads of stage s are done once at most the later
+        // stages' loads are outstanding; the barrier publishes every wave's
+        // loads and retires the reads of the buffer refilled next
+        wait_stages_barrier<C::kSegPer, C::kBuf - 2>(n_stages_g - 1 - s);
+        const int nbuf = buf == 0 ? C::kBuf - 1 : buf - 1;
+
+        const unsigned char* st = smem + buf * C::kStageBytes;
+        const uint16_t* sa = reinterpret_cast<const uint16_t*>(st) + (kg * C::BM + wm * TM * 32 + r_lane) * kRow;
+        const uint16_t* sb = reinterpret_cast<const uint16_t*>(st + C::kAStageBytes) +
+                             (kg * C::BN + wn * TN * 32 + r_lane) * kRow;
+        // packed A: the stage's 64 bits of each of this lane's rows; slice kk,
+        // half g reads byte 2*kk + g (K values 16*kk + 8*g ..)
+        u32x2 pa[TM];
+        if constexpr (PK) {
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+            pa[i] = *reinterpret_cast<const u32x2*>(st + (kg * C::BM + wm * TM * 32 + i * 32 + r_lane) * 8);
+        }
+        auto read = [&](bf16x8 (&fa)[TM], bf16x8 (&fb)[TN], int kk) {
+          // tile rows start at multiples of 32, so the swizzle depends on r_lane only
+          const int ch = swz(r_lane, kk * 2 + g_lane) * 8;
+#pragma unroll
+          for (int i = 0; i < TM; ++i) {
+            if constexpr (PK) {
+              const u32x4 e = bits_to_bf16x8((pa[i][kk >> 1] >> (16 * (kk & 1) + 8 * g_lane)) & 0xFFu);
+              __builtin_memcpy(&fa[i], &e, 16);
+            } else {
+              fa[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kRow + ch);
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRow + ch);
+        };
+        // software pipeline over the k-slices: the reads of slice kk+1 and a
+        // share of the next stage's loads are in flight while slice kk's MFMAs
+        // run (the compiler's own interleaving measured 3-6% faster than
+        // scheduling barriers around each MFMA group)
+        bf16x8 fa[2][TM], fb[2][TN];
+        read(fa[0], fb[0], 0);
+#pragma unroll
+        for (int kk = 0; kk < kSlices; ++kk) {
+          if (kk + 1 < kSlices) read(fa[(kk + 1) & 1], fb[(kk + 1) & 1], kk + 1);
+#pragma unroll
+          for (int i = 0; i < C::kSegPer; ++i)
+            if (i % kSlices == kk) issue_seg(sp, i, nbuf);
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
+        }
+        sp = prepare(s + C::kBuf);
+        buf = buf + 1 == C::kBuf ? 0 : buf + 1;
+      }
+      // every wave is done reading the ring before LDS is reused
+      wait_vmcnt_barrier<0>();
     }
-    // every wave is done reading the ring before LDS is reused
-    wait_vmcnt_barrier<0>();
 
     // ---- split-K reduction through LDS ----------------------------------
     if constexpr (KSPLIT > 1) {
@@ -791,13 +911,22 @@ void conv3x3_kernel(ConvArgs a) {
 template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int MODE, int TAPS,
           bool PK>
 int launch_cfg(const ConvArgs& a, hipStream_t stream) {
-  using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF, PK>;
-  const int64_t per_xcd = (static_cast<int64_t>(a.tiles_m) * a.tiles_n * a.splits + 7) / 8;
-  if (per_xcd * 8 > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
-  hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, NBUF, POOL, MODE, TAPS, PK>),
-                     dim3(static_cast<unsigned>(per_xcd * 8)), dim3(C::kThreads), 0, stream, a);
-  return launch_status();
+  if constexpr (NBUF == 0 && !PK) {
+    return SNNK_EUNSUPPORTED;  // resident weights read packed spikes only
+  } else {
+    using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF, PK>;
+    if (C::kRes && (a.splits != 1 || a.Cin % kKS != 0 || a.n_stages > C::kResStages))
+      return SNNK_EUNSUPPORTED;
+    const int64_t per_xcd = (static_cast<int64_t>(a.tiles_m) * a.tiles_n * a.splits + 7) / 8;
+    if (per_xcd * 8 > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
+    hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, NBUF, POOL, MODE, TAPS, PK>),
+                       dim3(static_cast<unsigned>(per_xcd * 8)), dim3(C::kThreads), 0, stream, a);
+    return launch_status();
+  }
 }
+
+// tile configurations from this one on keep their weights resident (NBUF = 0)
+constexpr int kFirstResCfg = 29;
 
 struct Plan {
   int cfg, splits, stages_per_split, tiles_m, tiles_n;
@@ -813,7 +942,9 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
   a.div_tiles_n = make_fastdiv(static_cast<uint32_t>(std::max(1, p.tiles_n)));
   a.splits = p.splits;
   a.stages_per_split = p.stages_per_split;
-  a.n_major = p.splits == 1 && a.w_bytes > a.x_bytes ? 1 : 0;
+  // (resident-weight tiles: Cout-tile major, so that each XCD fills its
+  // blocks' LDS from one or two weight slices held in its L2)
+  a.n_major = p.splits == 1 && (a.w_bytes > a.x_bytes || p.cfg >= kFirstResCfg) ? 1 : 0;
   a.tickets = static_cast<unsigned int*>(workspace);
   a.partials = p.splits > 1
       ? reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + p.ticket_bytes) : nullptr;
@@ -853,6 +984,20 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
     case 26: return launch_cfg<1, 1, 1, 2, 2, 5, POOL, MODE, TAPS, PK>(a, s);  // 32 x 64 split-K 2, 120 KB
     case 27: return launch_cfg<2, 2, 1, 2, 1, 5, POOL, MODE, TAPS, PK>(a, s);  // 64 x 128, 120 KB
     case 28: return launch_cfg<1, 2, 1, 2, 2, 4, POOL, MODE, TAPS, PK>(a, s);  // 32 x 128 split-K 2, 160 KB
+    // resident weights (packed x only): all of K of the block's weight rows
+    // in LDS, K up to 160 KB / (2 * BN)
+    case 29: return launch_cfg<8, 1, 2, 2, 1, 0, POOL, MODE, TAPS, PK>(a, s);  // 512 x 64, K <= 1280
+    case 30: return launch_cfg<4, 1, 2, 2, 1, 0, POOL, MODE, TAPS, PK>(a, s);  // 256 x 64, K <= 1280
+    case 31: return launch_cfg<8, 1, 2, 1, 1, 0, POOL, MODE, TAPS, PK>(a, s);  // 512 x 32, K <= 2560
+    case 32: return launch_cfg<4, 1, 2, 4, 1, 0, POOL, MODE, TAPS, PK>(a, s);  // 256 x 128, K <= 640
+    case 33: return launch_cfg<4, 1, 2, 1, 1, 0, POOL, MODE, TAPS, PK>(a, s);  // 256 x 32, K <= 2560
+    case 34: return launch_cfg<8, 1, 1, 2, 1, 0, POOL, MODE, TAPS, PK>(a, s);  // 256 x 64, K <= 1280
+    // sixteen waves (four per SIMD), 32 rows each
+    case 35: return launch_cfg<16, 1, 1, 2, 1, 0, POOL, MODE, TAPS, PK>(a, s);  // 512 x 64, K <= 1280
+    case 36: return launch_cfg<16, 1, 1, 1, 1, 0, POOL, MODE, TAPS, PK>(a, s);  // 512 x 32, K <= 2560
+    case 37: return launch_cfg<8, 1, 1, 1, 1, 0, POOL, MODE, TAPS, PK>(a, s);   // 256 x 32, K <= 2560
+    // 128 weight columns per wave (each expanded spike fragment feeds four MFMAs)
+    case 38: return launch_cfg<8, 1, 1, 4, 1, 0, POOL, MODE, TAPS, PK>(a, s);   // 256 x 128, K <= 640
     default: return SNNK_EINVAL;
   }
 }
