@@ -8,7 +8,7 @@ operands they must equal the bf16-input path of tile 2 (128 x 128, one K
 group, no split) bit for bit: fp32 pre-activations, spikes and packed words.
 Cases cover partial row tiles, Cout past the last full column tile, T past a
 multiple of 4 (several 4-step chunks), steps past T inside a chunk, the
-largest K each tile holds, and the shapes they refuse.
+largest K each tile holds, cross-block K splits, and the shapes they refuse.
 """
 import numpy as np
 import pytest
@@ -102,6 +102,45 @@ def test_resident_linear_equals_unsplit_bf16_tile(T, R, K, N, tile):
     assert torch.equal(linear_bias_lif_act(xp, w, b, **kw).cpu(), _pack(ref))
 
 
+SPLIT = [  # conv (T, B, Cin, Cout, H, W, pool) or Linear (T, R, K, N), tile, splits
+    ((4, 8, 256, 512, 4, 4, False), 37, 2),   # VGG L8 at batch 8
+    ((4, 8, 512, 512, 4, 4, True), 37, 2),    # L10: K = 4608 in two halves
+    ((3, 4, 512, 256, 4, 4, False), 36, 3),
+    ((5, 2, 256, 128, 4, 4, True), 35, 4),    # two chunks of 4 steps
+    ((4, 32, 2048, 2048), 37, 4),             # L11 as a dense Linear over 2x2 pixels
+    ((4, 32, 4096, 1024), 35, 4),             # FC2's K
+    ((4, 20, 512, 4096), 34, 2),              # FC1's shape, partial row tile
+]
+
+
+@pytest.mark.parametrize("shape,tile,splits", SPLIT)
+def test_resident_tiles_with_split_k_equal_bf16_split(shape, tile, splits):
+    """Cross-block split K on resident tiles: each block holds its share of the
+    K stages; the partial sums are reduced in split order, as in tile 2 with
+    the same split, so the results agree bit for bit."""
+    print(f"[resident split] {shape} tile {tile} splits {splits}", flush=True)
+    ref_kw, kw = dict(tile_hint=2, splits=splits), dict(tile_hint=tile, splits=splits)
+    if len(shape) == 7:
+        T, B, Cin, Cout, H, W, pool = shape
+        x, wp, bd = _conv_case(T, B, Cin, Cout, H, W, seed=Cin + Cout + splits, p=0.15)
+        xd, xp = x.to(DEV), _pack(x).to(DEV)
+        ref = kc.conv3x3_bn_lif_nhwc(xd, wp, bd, pool=pool, **ref_kw, **LIF).cpu()
+        got = kc.conv3x3_bn_lif_act(xp, wp, bd, pool=pool, **kw, **LIF).cpu()
+    else:
+        T, R, K, N = shape
+        g = torch.Generator().manual_seed(K + N + splits)
+        x = (torch.rand(T, R, K, generator=g) < 0.2).to(torch.bfloat16)
+        w = (torch.randn(N, K, generator=g) * (2.0 / K) ** 0.5 * 2.0).to(DEV, torch.bfloat16)
+        b = (torch.randn(N, generator=g) * 0.1).to(DEV)
+        xd, xp = x.to(DEV), _pack(x).to(DEV)
+        pre = linear_preact(xd, w, b, **ref_kw).cpu()
+        assert torch.equal(linear_preact_act(xp, w, b, **kw).cpu(), pre)
+        ref = linear_bias_lif(xd, w, b, **ref_kw, **LIF).cpu()
+        got = linear_bias_lif_act(xp, w, b, **kw, **LIF).cpu()
+    assert 0 < int(ref.float().sum()) < ref.numel()
+    assert torch.equal(got, _pack(ref))
+
+
 def test_resident_tiles_refuse_what_they_do_not_hold():
     x, wp, bd = _conv_case(4, 1, 96, 64, 4, 4, seed=1)
     with pytest.raises(SnnkError):   # Cin % 64 != 0: a stage would span two taps
@@ -111,5 +150,6 @@ def test_resident_tiles_refuse_what_they_do_not_hold():
         kc.conv3x3_bn_lif_act(_pack(x).to(DEV), wp, bd, pool=False, tile_hint=29, splits=1, **LIF)
     with pytest.raises(SnnkError):   # bf16 input
         kc.conv3x3_bn_lif_act(x.to(DEV), wp, bd, pool=False, tile_hint=31, splits=1, **LIF)
-    with pytest.raises(SnnkError):   # split K
-        kc.conv3x3_bn_lif_act(_pack(x).to(DEV), wp, bd, pool=False, tile_hint=31, splits=2, **LIF)
+    with pytest.raises(SnnkError):   # 2304 / 2 = 1152 fits 64 columns, but 4608 / 2 does not
+        x5, wp5, bd5 = _conv_case(4, 1, 512, 64, 4, 4, seed=3)
+        kc.conv3x3_bn_lif_act(_pack(x5).to(DEV), wp5, bd5, pool=False, tile_hint=29, splits=2, **LIF)

@@ -213,8 +213,7 @@ int make_plan(const ConvArgs& a, int tile_hint, int splits_hint, bool allow_spli
   if (allow_split) {
     if (splits_hint > 0) splits = splits_hint;
     else if (tile_hint < 0) splits = auto_splits;
-    else if (mn < 160 && p->cfg < kFirstResCfg)  // fill the GPU (resident weights: no split)
-      splits = static_cast<int>((256 + mn - 1) / mn);
+    else if (mn < 160) splits = static_cast<int>((256 + mn - 1) / mn);  // fill the GPU
     // at least 4 K stages per split; tile ids must fit the ticket region
     splits = std::max(1, std::min(splits, a.n_stages / 4));
     if (mn > kMaxTickets) splits = 1;

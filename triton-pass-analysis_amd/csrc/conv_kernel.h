@@ -146,8 +146,9 @@ struct Cfg {
   // NBUF = 0: resident weights.  The block's BN weight rows stay in LDS for
   // all K (loaded once), and each lane loads the packed spike words of its
   // own A rows straight into registers a few stages ahead: the K loop has no
-  // barrier and no LDS ring.  Packed A only, one K group, K % 64 == 0 and
-  // K * BN * 2 <= kResBytes.
+  // barrier and no LDS ring.  Packed A only, one K group, Cin % 64 == 0 and
+  // the block's K stages (all of K, or its share under a cross-block split)
+  // times BN rows of 128 bytes within kResBytes.
   static constexpr bool kRes = NBUF == 0;
   static_assert(!kRes || (PK && KSPLIT == 1), "resident weights: packed A, one K group");
   // operand stages arrive by direct-to-LDS loads; the WM*WN waves of a K
@@ -518,16 +519,17 @@ void conv3x3_kernel(ConvArgs a) {
 
   // ---- resident weights: one fill, then K loops without barriers ----------
   if constexpr (C::kRes) {
-    // fill segment g: weight rows 8*(g % kSegB).. of K stage g / kSegB, one
-    // 16-byte chunk per lane, swizzled as in the ring; LDS stage s holds the
-    // block's BN rows at 128 bytes each
-    const int n_seg = a.n_stages * C::kSegB;
+    // fill segment g: weight rows 8*(g % kSegB).. of the block's K stage
+    // g / kSegB (global stage st_begin + g / kSegB), one 16-byte chunk per
+    // lane, swizzled as in the ring; LDS slot s holds the block's BN rows of
+    // its stage s at 128 bytes each
+    const int n_seg = (st_end - st_begin) * C::kSegB;
     for (int g = wave; g < n_seg; g += C::kWaves) {
       const int st = g / C::kSegB;
       const int n = 8 * (g - st * C::kSegB) + lrow;
       const uint32_t off = n0 + n < a.Cout
                                ? static_cast<uint32_t>(n0 + n) * static_cast<uint32_t>(K) * 2u +
-                                     static_cast<uint32_t>(st) * kRowBytes + swz(n, slot) * 16u
+                                     static_cast<uint32_t>(st_begin + st) * kRowBytes + swz(n, slot) * 16u
                                : kFar;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           wr, (lds_ptr_t)(smem + (st * C::BN + n - lrow) * kRowBytes), 16, off, 0, 0, 0);
@@ -541,11 +543,11 @@ void conv3x3_kernel(ConvArgs a) {
   constexpr int kAhead = 3;
   auto res_k_loop = [&](f32x16 (&acc)[TM][TN], int tc, bool t_ok, uint32_t chunk_off)
                         __attribute__((always_inline)) {
-    const int n_st = a.n_stages;
+    const int n_st = st_end - st_begin;  // this block's K stages (all of K without a split)
     uint32_t a_off[TM];
     int cur_tap = -1;
     auto load_a = [&](int s, u32x2 (&dst)[TM]) __attribute__((always_inline)) {
-      const uint32_t k0 = static_cast<uint32_t>(s) * kKS;
+      const uint32_t k0 = static_cast<uint32_t>(st_begin + s) * kKS;
       const int tap = static_cast<int>(fdiv(k0, a.div_cin));
       const int cin_lo = static_cast<int>(k0) - tap * a.Cin;
       if (tap != cur_tap) {  // every Cin / 64 stages
@@ -915,7 +917,7 @@ int launch_cfg(const ConvArgs& a, hipStream_t stream) {
     return SNNK_EUNSUPPORTED;  // resident weights read packed spikes only
   } else {
     using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF, PK>;
-    if (C::kRes && (a.splits != 1 || a.Cin % kKS != 0 || a.n_stages > C::kResStages))
+    if (C::kRes && (a.Cin % kKS != 0 || a.stages_per_split > C::kResStages))
       return SNNK_EUNSUPPORTED;
     const int64_t per_xcd = (static_cast<int64_t>(a.tiles_m) * a.tiles_n * a.splits + 7) / 8;
     if (per_xcd * 8 > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
