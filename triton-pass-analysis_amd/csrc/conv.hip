@@ -135,21 +135,24 @@ bool auto_cfg_packed(const ConvArgs& a, bool taps9, int* cfg, int* splits) {
   *splits = 1;
   // Resident-weight tiles for the 3x3 layers with many rows, from sweeps at
   // batch 8, 32 and 56 (conv config at batch 32: 20.7 us against 23.5; VGG
-  // L2-L7 20-24% faster): the tile whose count fills the 256 CUs best (tiles
-  // / whole waves of 256 blocks), ties to 64 weight columns, then 512 rows.
-  // Below half a wave of blocks, or below 8192 rows (batch 1), the streamed
-  // tiles are faster.
+  // L2-L7 20-24% faster).  Score: how well the tile count fills the 256 CUs
+  // (tiles / whole waves of 256 blocks), weighted 0.55 for 32-column tiles,
+  // whose waves expand each spike fragment for one MFMA instead of two (VGG
+  // L2 at batch 56: 256x32 tiles fill 1.0 and take 42 us, 512x64 fill 0.875
+  // and take 25); ties to 64 columns, then 512 rows.  Below half a wave of
+  // blocks, or below 8192 rows (batch 1), the streamed tiles are faster.
   if (taps9 && rows >= 8192 && a.Cin % kKS == 0) {
     struct Res { int cfg, bm, bn; };
     constexpr Res kRes[] = {{35, 512, 64}, {34, 256, 64}, {31, 512, 32}, {37, 256, 32}};
     int best = -1;
-    double best_fill = 0.0;
+    double best_score = 0.0, best_fill = 0.0;
     for (const Res& r : kRes) {
       if (K * r.bn * 2 > kResBytes) continue;
       const int64_t tiles = ((a.n_quads + r.bm / 16 - 1) / (r.bm / 16)) *
                             ((a.Cout + r.bn - 1) / r.bn);
       const double fill = static_cast<double>(tiles) / (((tiles + 255) / 256) * 256);
-      if (fill > best_fill + 1e-9) { best = r.cfg; best_fill = fill; }
+      const double score = fill * (r.bn >= 64 ? 1.0 : 0.55);
+      if (score > best_score + 1e-9) { best = r.cfg; best_score = score; best_fill = fill; }
     }
     if (best >= 0 && best_fill >= 0.5) { *cfg = best; return true; }
   }
