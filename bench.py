@@ -537,13 +537,15 @@ def _vgg_layer_steps(eng, image, T):
                            ("FC2", eng.fc2_w, eng.fc2_b, False),
                            ("FC3", eng.fc3_w, eng.fc3_b, True)):
         fin = f
+        # as the engine: FC1 writes packed words when spikes travel packed
+        ob = bits and nm == "FC1"
         if last:
             f = linear_mean_t(fin, w, b)
             fn = (lambda a=fin, w=w, b=b, o=torch.empty_like(f): linear_mean_t(a, w, b, out=o))
-        elif fin.dtype == torch.int32:
-            f = linear_bias_lif_act(fin, w, b, out_bits=False, **lif)
-            fn = (lambda a=fin, w=w, b=b, o=torch.empty_like(f):
-                  linear_bias_lif_act(a, w, b, out_bits=False, out=o, **lif))
+        elif fin.dtype == torch.int32 or ob:
+            f = linear_bias_lif_act(fin, w, b, out_bits=ob, **lif)
+            fn = (lambda a=fin, w=w, b=b, ob=ob, o=torch.empty_like(f):
+                  linear_bias_lif_act(a, w, b, out_bits=ob, out=o, **lif))
         else:
             f = linear_bias_lif(fin, w, b, **lif)
             fn = (lambda a=fin, w=w, b=b, o=torch.empty_like(f):
@@ -560,7 +562,7 @@ def _vgg_teacher_forced(eng, params, img_cpu, T, dev):
     (packed words into the conv layers); FC3: max |logit error|."""
     from snnk.kernels.binary import pack_bits
     from snnk.kernels.conv import conv3x3_image_lif, to_nhwc_bf16
-    from snnk.kernels.linear import linear_bias_lif, linear_preact
+    from snnk.kernels.linear import linear_bias_lif, linear_bias_lif_act, linear_preact
     from oracle import vgg as ov
 
     B = img_cpu.shape[0]
@@ -586,8 +588,16 @@ def _vgg_teacher_forced(eng, params, img_cpu, T, dev):
             name = "L%d" % (len(out) + 1)
         elif r["kind"] == "fc_lif":
             w, b = fcs.pop(0)
+            first = len(fcs) == 1
             xp = torch.nn.functional.pad(r["input"], (0, 0, 0, R - B))
-            y = linear_bias_lif(xp.to(dev, torch.bfloat16).contiguous(), w, b, **lif)[:, :B]
+            xp = xp.to(dev, torch.bfloat16).contiguous()
+            # the engine's formats: FC1 bf16 in, packed words out; FC2 packed in
+            if eng.bits_between_layers:
+                xin = xp if first else pack_bits(xp, dim=-1)
+                y = linear_bias_lif_act(xin, w, b, out_bits=first, **lif)
+                y = (_unpack_words(y, w.shape[0]) if first else y.float())[:, :B]
+            else:
+                y = linear_bias_lif(xp, w, b, **lif)[:, :B]
             out.append({"layer": "FC%d" % (3 - len(fcs) - 1),
                         "agreement": (y.cpu().float() == r["output"]).float().mean().item(),
                         "rate": r["output"].mean().item()})

@@ -39,7 +39,7 @@
 namespace snnk {
 namespace {
 
-constexpr int kNumTiles = 39;
+constexpr int kNumTiles = 42;
 struct TileShape { int bm, bn; };
 //                                   0          1         2          3         4        5
 constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 128}, {32, 32}, {32, 128},
@@ -51,7 +51,9 @@ constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 
     {256, 64}, {128, 128}, {128, 128}, {32, 32}, {32, 64}, {64, 128}, {32, 128},
 //   29 - 38: resident weights, packed x only
     {512, 64}, {256, 64}, {512, 32}, {256, 128}, {256, 32}, {256, 64}, {512, 64}, {512, 32},
-    {256, 32}, {256, 128}};
+    {256, 32}, {256, 128},
+//   39         40         41
+    {64, 64}, {64, 64}, {64, 64}};
 
 // Tile shape by problem size (rows = output rows of one 4-step chunk, K =
 // 9*Cin or the Linear depth): big tiles while M fills 256 CUs, split-K wave
@@ -161,9 +163,14 @@ bool auto_cfg_packed(const ConvArgs& a, bool taps9, int* cfg, int* splits) {
     // K = 384, 1152 columns: 17.8 us with 128 x 64 tiles, 21.9 with 128 x 128)
     if (rows >= 8192 && K <= 512) { *cfg = a.Cout > 512 ? 10 : 9; return true; }
     if (rows <= 64 || rows > 256) return false;
-    if (K >= 4096) { *cfg = rows <= 128 ? 7 : 12; *splits = rows <= 128 ? 2 : 3; return true; }
-    if (K >= 2048) { if (rows <= 128) return false; *cfg = 7; *splits = 2; return true; }
-    if (K <= 512) { *cfg = rows <= 128 ? 4 : 7; return true; }
+    // FC2 (K = 4096): 32x32 tiles with 4 K groups at batch 32 (13.5 us against
+    // 15.2 with 32x64 tiles and 2 splits), 64x64 with 4 groups at batch 56
+    // (16.6 against 21.3); the dense 2x2 layers (K = 2048) at batch 56: 32x32
+    // tiles, 4 groups, no split (9.1 us against 11.8); FC1 (K = 512, 4096
+    // columns) at batch 56: 64x64 tiles, 2 groups (7.4 against 8.0)
+    if (K >= 4096) { *cfg = rows <= 128 ? 4 : 39; return true; }
+    if (K >= 2048) { if (rows <= 128) return false; *cfg = 4; return true; }
+    if (K <= 512) { *cfg = rows <= 128 ? 4 : a.Cout > 512 ? 41 : 7; return true; }
     return false;
   }
   if (rows >= 65536) {                            // VGG L2 at batch 32 / 56
@@ -188,10 +195,11 @@ bool auto_cfg_packed(const ConvArgs& a, bool taps9, int* cfg, int* splits) {
   }
   if (rows >= 2048) {                             // L8 - L10
     if (K <= 1152) { *cfg = 4; return true; }
-    if (rows <= 2048) { *cfg = 7; return true; }
-    if (K <= 2304) { *cfg = 5; return true; }
-    *cfg = pool ? 10 : 12;
-    *splits = 2;
+    // 64x64 tiles, K over 4 wave groups at batch 32 (2048 rows: L9 18.5 us
+    // against 20.9 with 32x64 tiles) and over 2 at batch 56 (L10 26.3 against
+    // 29.5 with 128x64 tiles and 2 splits): each weight byte is re-read by
+    // half as many row tiles as with 32-row tiles
+    *cfg = rows <= 2048 ? 39 : 41;
     return true;
   }
   return false;

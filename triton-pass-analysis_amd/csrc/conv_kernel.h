@@ -175,7 +175,10 @@ struct Cfg {
   static constexpr int kLdsBytes = kRes ? kResBytes : kBuf * kStageBytes;
   static constexpr int kRedBytes = (KSPLIT - 1) * WM * WN * TM * TN * 16 * 64 * 4;
   static constexpr int kSmem = kLdsBytes > kRedBytes ? kLdsBytes : kRedBytes;
-  static_assert((kRes || NBUF >= 2) && kSmem <= 160 * 1024, "LDS ring must fit 160 KB");
+  static_assert(kRes || NBUF >= 2, "ring depth");
+  // the LDS the block needs fits the CU's 160 KB (some tiles fit only with
+  // packed A: launch_cfg refuses their bf16 form)
+  static constexpr bool kFits = kSmem <= 160 * 1024;
   // K stages of the resident weights that fit
   static constexpr int kResStages = kResBytes / (BN * kRowBytes);
 };
@@ -213,6 +216,7 @@ template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int M
 __global__ __launch_bounds__(64 * WM * WN * KSPLIT)
 void conv3x3_kernel(ConvArgs a) {
   using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF, PK>;
+  static_assert(C::kFits, "LDS ring must fit 160 KB");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::kSmem];
 
   const int tid = threadIdx.x;
@@ -915,6 +919,8 @@ template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int M
 int launch_cfg(const ConvArgs& a, hipStream_t stream) {
   if constexpr (NBUF == 0 && !PK) {
     return SNNK_EUNSUPPORTED;  // resident weights read packed spikes only
+  } else if constexpr (!Cfg<WM, WN, TM, TN, KSPLIT, NBUF, PK>::kFits) {
+    return SNNK_EUNSUPPORTED;  // this tile's ring does not fit LDS in this A format
   } else {
     using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF, PK>;
     if (C::kRes && (a.Cin % kKS != 0 || a.stages_per_split > C::kResStages))
@@ -1000,6 +1006,12 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
     case 37: return launch_cfg<8, 1, 1, 1, 1, 0, POOL, MODE, TAPS, PK>(a, s);   // 256 x 32, K <= 2560
     // 128 weight columns per wave (each expanded spike fragment feeds four MFMAs)
     case 38: return launch_cfg<8, 1, 1, 4, 1, 0, POOL, MODE, TAPS, PK>(a, s);   // 256 x 128, K <= 640
+    // 64-row ring tiles with K spread over 2-8 wave groups, for the layers
+    // with few rows and long K (each weight byte re-read by half as many row
+    // tiles as with 32-row tiles)
+    case 39: return launch_cfg<2, 1, 1, 2, 4, 3, POOL, MODE, TAPS, PK>(a, s);   // 64 x 64 split-K 4
+    case 40: return launch_cfg<2, 1, 1, 2, 8, 2, POOL, MODE, TAPS, PK>(a, s);   // 64 x 64 split-K 8
+    case 41: return launch_cfg<2, 1, 1, 2, 2, 4, POOL, MODE, TAPS, PK>(a, s);   // 64 x 64 split-K 2
     default: return SNNK_EINVAL;
   }
 }

@@ -300,12 +300,17 @@ class FusedVGGSNN(nn.Module):
         R = (B + 3) // 4 * 4
         if R != B:
             x = F.pad(x, (0, 0, 0, R - B))
-        # FC1 takes the features in whichever format the last conv wrote
-        x = (linear_bias_lif_act(x, self.fc1_w, self.fc1_b, out_bits=False, **self._lif())
-             if x.dtype == torch.int32 else linear_bias_lif(x, self.fc1_w, self.fc1_b, **self._lif()))
+        # FC1 takes the features in whichever format the last conv wrote and,
+        # with packed spikes between layers, hands FC2 packed words; FC2 writes
+        # bf16 spikes for FC3 (its mean-over-T head reads bf16)
+        bits = self.bits_between_layers
+        x = (linear_bias_lif_act(x, self.fc1_w, self.fc1_b, out_bits=bits, **self._lif())
+             if x.dtype == torch.int32 or bits
+             else linear_bias_lif(x, self.fc1_w, self.fc1_b, **self._lif()))
         if rates is not None:
-            rates.append(x[:, :B].float().mean())
-        x = linear_bias_lif(x, self.fc2_w, self.fc2_b, **self._lif())
+            rates.append(spike_rate(x[:, :B]))
+        x = (linear_bias_lif_act(x, self.fc2_w, self.fc2_b, out_bits=False, **self._lif())
+             if x.dtype == torch.int32 else linear_bias_lif(x, self.fc2_w, self.fc2_b, **self._lif()))
         if rates is not None:
             rates.append(x[:, :B].float().mean())
         if mean_t:
