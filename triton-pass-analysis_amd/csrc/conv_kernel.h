@@ -806,27 +806,40 @@ void conv3x3_kernel(ConvArgs a) {
 
     // ---- split-K reduction through LDS ----------------------------------
     if constexpr (KSPLIT > 1) {
-      float* red = reinterpret_cast<float*>(smem);
+      // 16-byte pieces, lane-contiguous (conflict-free ds_write_b128 /
+      // ds_read_b128); the reads of one row of tiles are all issued before
+      // the sums, so their LDS latencies overlap instead of adding up
+      f32x4* red = reinterpret_cast<f32x4*>(smem);
       if (kg > 0) {
-        float* dst = red + ((kg - 1) * WM * WN + wmn) * TM * TN * 16 * 64;
+        f32x4* dst = red + ((kg - 1) * WM * WN + wmn) * TM * TN * 4 * 64;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) dst[((i * TN + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+            for (int q = 0; q < 4; ++q)
+              dst[((i * TN + j) * 4 + q) * 64 + lane] =
+                  f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
       }
       __syncthreads();
       if (kg == 0) {
 #pragma unroll
         for (int gg = 1; gg < KSPLIT; ++gg) {
-          const float* src = red + ((gg - 1) * WM * WN + wmn) * TM * TN * 16 * 64;
+          const f32x4* src = red + ((gg - 1) * WM * WN + wmn) * TM * TN * 4 * 64;
 #pragma unroll
-          for (int i = 0; i < TM; ++i)
+          for (int i = 0; i < TM; ++i) {
+            f32x4 part[TN][4];
 #pragma unroll
             for (int j = 0; j < TN; ++j)
 #pragma unroll
-              for (int e = 0; e < 16; ++e) acc[i][j][e] += src[((i * TN + j) * 16 + e) * 64 + lane];
+              for (int q = 0; q < 4; ++q) part[j][q] = src[((i * TN + j) * 4 + q) * 64 + lane];
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[i][j][4 * q + c] += part[j][q][c];
+          }
         }
       }
       __syncthreads();
