@@ -69,18 +69,6 @@ __device__ __forceinline__ void wait_vmcnt_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// Wait for a ring stage whose `later` successors (at most MAXL, kSEG loads
-// each) may still be in flight; a stage past the end issues no loads, so the
-// tail of the K loop waits for fewer.
-template <int kSEG, int MAXL>
-__device__ __forceinline__ void wait_stages_barrier(int later) {
-  static_assert(MAXL >= 0 && MAXL <= 3, "ring depth");
-  if (later >= MAXL) wait_vmcnt_barrier<kSEG * MAXL>();
-  else if (later == 2) wait_vmcnt_barrier<kSEG * 2>();
-  else if (later == 1) wait_vmcnt_barrier<kSEG>();
-  else wait_vmcnt_barrier<0>();
-}
-
 // 16-byte chunk c of LDS row r is stored at chunk c ^ key(r).  gfx950 serves
 // a ds_read_b128 16 lanes per pass over 64 four-byte banks; the fragment
 // reads (16 consecutive rows, one chunk column) then hit 16 distinct 16-byte
@@ -640,21 +628,32 @@ void conv3x3_kernel(ConvArgs a) {
       for (int i = 0; i < C::kAPer; ++i) a_off[i] = kFar;
       int cur_lo = -1, cur_hi = -1;
 
-      // wave-uniform addressing of group-local stage sl
+      // wave-uniform addressing of the group's next stage to load.  The
+      // group's K stages lie KSPLIT apart, so the next one's tap and first
+      // channel follow from the last by an add and a compare (one division
+      // at the start of the chunk, none per stage)
       struct StageAddr {
         bool live;        // a stage of the ring loop (later slots are not loaded)
         bool zero_b;      // B reads zeros: a stage past the block's K range
         bool tail;        // the last stage of K % 64 == 32: upper half past K
         uint32_t da, db;  // A: chunk + channel bytes of the lower half; B: bytes of k0
       };
-      auto prepare = [&](int sl) {
+      int nx_sl = 0;                   // group-local index of the next stage
+      int nx_sg = st_begin + kg;       // its global K stage
+      int nx_tap, nx_cin;              // its tap and first channel: k0 = tap * Cin + cin
+      {
+        const uint32_t k0 = static_cast<uint32_t>(nx_sg * kKS);
+        nx_tap = static_cast<int>(fdiv(k0, a.div_cin));
+        nx_cin = static_cast<int>(k0) - nx_tap * a.Cin;
+      }
+      auto prepare_next = [&]() {
         StageAddr p;
-        const int sg = st_begin + sl * KSPLIT + kg;
-        p.live = sl < n_stages_g;
-        p.zero_b = sg >= st_end;
-        const uint32_t k0 = p.zero_b ? 0u : static_cast<uint32_t>(sg * kKS);
-        const int tap_lo = static_cast<int>(fdiv(k0, a.div_cin));
-        const int cin_lo = static_cast<int>(k0) - tap_lo * a.Cin;
+        p.live = nx_sl < n_stages_g;
+        p.zero_b = nx_sg >= st_end;
+        // (a stage past the K range reads as k0 = 0; its B offsets are kFar)
+        const int tap_lo = p.zero_b ? 0 : nx_tap;
+        const int cin_lo = p.zero_b ? 0 : nx_cin;
+        const uint32_t k0 = p.zero_b ? 0u : static_cast<uint32_t>(nx_sg * kKS);
         const bool wrap = cin_lo + 32 >= a.Cin;  // upper half starts the next tap
         const int tap_hi = tap_lo + (wrap ? 1 : 0);
         p.da = chunk_off + static_cast<uint32_t>(cin_lo) * 2u;
@@ -682,6 +681,14 @@ void conv3x3_kernel(ConvArgs a) {
             const bool ok = t_ok && ((s_ok[i] >> tap) & 1u);
             a_off[i] = ok ? s_base[i] + static_cast<uint32_t>(h ? del_hi : del_lo) : kFar;
           }
+        }
+        // step to the group's following stage
+        ++nx_sl;
+        nx_sg += KSPLIT;
+        nx_cin += KSPLIT * kKS;
+        while (nx_cin >= a.Cin) {
+          nx_cin -= a.Cin;
+          ++nx_tap;
         }
         return p;
       };
@@ -720,7 +727,7 @@ void conv3x3_kernel(ConvArgs a) {
       // instruction cache, so one copy of it is fetched instead of NBUF-1
 #pragma nounroll
       for (int p = 0; p < C::kBuf - 1; ++p) {
-        const StageAddr sp = prepare(p);
+        const StageAddr sp = prepare_next();
 #pragma unroll
         for (int i = 0; i < C::kSegPer; ++i) issue_seg(sp, i, p);
       }
@@ -744,12 +751,15 @@ void conv3x3_kernel(ConvArgs a) {
       // addressing of the stage the next iteration loads; prepared at the end
       // of the previous iteration, so that after each barrier the fragment
       // reads issue at once instead of behind the scalar stage arithmetic
-      StageAddr sp = prepare(C::kBuf - 1);
+      StageAddr sp = prepare_next();
       for (int s = 0; s < n_stages_g; ++s) {
-        // this wave's loads of stage s are done once at most the later
-        // stages' loads are outstanding; the barrier publishes every wave's
-        // loads and retires the reads of the buffer refilled next
-        wait_stages_barrier<C::kSegPer, C::kBuf - 2>(n_stages_g - 1 - s);
+        // every ring iteration (and the prologue, per stage) issues kSegPer
+        // loads, past the end of K as well, so this wave's loads of stage s
+        // are done once at most the kBuf - 2 later stages' loads are
+        // outstanding; the barrier publishes every wave's loads and retires
+        // the reads of the buffer refilled next
+        static_assert(C::kSegPer * (C::kBuf - 2) <= 63, "vmcnt holds 6 bits");
+        wait_vmcnt_barrier<C::kSegPer * (C::kBuf - 2)>();
         const int nbuf = buf == 0 ? C::kBuf - 1 : buf - 1;
 
         const unsigned char* st = smem + buf * C::kStageBytes;
@@ -797,7 +807,7 @@ void conv3x3_kernel(ConvArgs a) {
             for (int j = 0; j < TN; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
         }
-        sp = prepare(s + C::kBuf);
+        sp = prepare_next();
         buf = buf + 1 == C::kBuf ? 0 : buf + 1;
       }
       // every wave is done reading the ring before LDS is reused
