@@ -161,7 +161,9 @@ struct Cfg {
   static constexpr int kStageBytes = kAStageBytes + KSPLIT * BN * kRowBytes;
   static constexpr int kBuf = NBUF;  // ring of operand stages in LDS
   static constexpr int kLdsBytes = kRes ? kResBytes : kBuf * kStageBytes;
-  static constexpr int kRedBytes = (KSPLIT - 1) * WM * WN * TM * TN * 16 * 64 * 4;
+  // K-group sums: a slot per (group, wave, tile) for the tiles another
+  // group finishes
+  static constexpr int kRedBytes = KSPLIT > 1 ? KSPLIT * WM * WN * TM * TN * 16 * 64 * 4 : 0;
   static constexpr int kSmem = kLdsBytes > kRedBytes ? kLdsBytes : kRedBytes;
   static_assert(kRes || NBUF >= 2, "ring depth");
   // the LDS the block needs fits the CU's 160 KB (some tiles fit only with
@@ -341,7 +343,14 @@ void conv3x3_kernel(ConvArgs a) {
   const int n_stages_g = (st_end - st_begin + KSPLIT - 1) / KSPLIT;
   const int n_chunks = (a.T + 3) / 4;
 
-  // membrane state of the epilogue waves: [TM][TN][4 pixels]
+  // With K groups, accumulator tile (i, j) of wave wmn is summed and
+  // finished (LIF epilogue, or split-K partials) by the wave wmn of group
+  // (i*TN + j) % KSPLIT: the epilogue work of a block is spread over its
+  // groups instead of falling to group 0 alone.
+  auto mine = [&](int i, int j) __attribute__((always_inline)) {
+    return KSPLIT == 1 || (i * TN + j) % KSPLIT == kg;
+  };
+  // membrane state of the tiles this wave finishes: [TM][TN][4 pixels]
   float v[TM][TN][4];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -394,7 +403,7 @@ void conv3x3_kernel(ConvArgs a) {
       if (quad >= a.n_quads) continue;
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        if (!col_ok[j]) continue;
+        if (!col_ok[j] || !mine(i, j)) continue;
         const int n = n0 + (wn * TN + j) * 32 + r_lane;
         // TAPS = 1 with POOL: the output keeps one column of every group of
         // four adjacent columns (their OR), Cout / 4 columns per row
@@ -455,7 +464,7 @@ void conv3x3_kernel(ConvArgs a) {
       }
     }
   };
-  // the LIF epilogue, or the fp32 pre-activations; run by the kg == 0 waves
+  // the LIF epilogue, or the fp32 pre-activations, of the tiles this wave finishes
   // (both lambdas are forced inline: a call would move the accumulators to scratch)
   auto epilogue = [&](const f32x16 (&acc)[TM][TN], int tc) __attribute__((always_inline)) {
     if constexpr (MODE == MODE_PREACT) {
@@ -465,7 +474,7 @@ void conv3x3_kernel(ConvArgs a) {
         if (quad >= a.n_quads) continue;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          if (!col_ok[j]) continue;
+          if (!col_ok[j] || !mine(i, j)) continue;
           const int n = n0 + (wn * TN + j) * 32 + r_lane;
 #pragma unroll
           for (int q = 0; q < 4; ++q)
@@ -488,7 +497,7 @@ void conv3x3_kernel(ConvArgs a) {
         if (quad >= a.n_quads) continue;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          if (!col_ok[j]) continue;
+          if (!col_ok[j] || !mine(i, j)) continue;
           const int n = n0 + (wn * TN + j) * 32 + r_lane;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -816,46 +825,59 @@ void conv3x3_kernel(ConvArgs a) {
 
     // ---- split-K reduction through LDS ----------------------------------
     if constexpr (KSPLIT > 1) {
-      // 16-byte pieces, lane-contiguous (conflict-free ds_write_b128 /
-      // ds_read_b128); the reads of one row of tiles are all issued before
-      // the sums, so their LDS latencies overlap instead of adding up
+      // Each wave parks the tiles another group finishes in its LDS slots
+      // (16-byte pieces, lane-contiguous: conflict-free ds_write_b128 /
+      // ds_read_b128), then sums the tiles it finishes in group order,
+      // ((g0 + g1) + g2) + ..., each group's four reads issued before its adds
       f32x4* red = reinterpret_cast<f32x4*>(smem);
-      if (kg > 0) {
-        f32x4* dst = red + ((kg - 1) * WM * WN + wmn) * TM * TN * 4 * 64;
+      auto slot = [&](int g, int i, int j) __attribute__((always_inline)) {
+        return red + ((g * WM * WN + wmn) * TM * TN + i * TN + j) * 4 * 64 + lane;
+      };
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN; ++j) {
+          if (mine(i, j)) continue;
+          f32x4* dst = slot(kg, i, j);
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              dst[((i * TN + j) * 4 + q) * 64 + lane] =
-                  f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-      }
+          for (int q = 0; q < 4; ++q)
+            dst[q * 64] = f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        }
       __syncthreads();
-      if (kg == 0) {
 #pragma unroll
-        for (int gg = 1; gg < KSPLIT; ++gg) {
-          const f32x4* src = red + ((gg - 1) * WM * WN + wmn) * TM * TN * 4 * 64;
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int i = 0; i < TM; ++i) {
-            f32x4 part[TN][4];
+        for (int j = 0; j < TN; ++j) {
+          if (!mine(i, j)) continue;
+          f32x16 sum;
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
+          for (int g = 0; g < KSPLIT; ++g) {
+            f32x16 part;
+            if (g == kg) {
+              part = acc[i][j];
+            } else {
+              const f32x4* src = slot(g, i, j);
+              f32x4 pc[4];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) part[j][q] = src[((i * TN + j) * 4 + q) * 64 + lane];
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
+              for (int q = 0; q < 4; ++q) pc[q] = src[q * 64];
 #pragma unroll
               for (int q = 0; q < 4; ++q)
 #pragma unroll
-                for (int c = 0; c < 4; ++c) acc[i][j][4 * q + c] += part[j][q][c];
+                for (int c = 0; c < 4; ++c) part[4 * q + c] = pc[q][c];
+            }
+            if (g == 0) {
+              sum = part;
+            } else {
+#pragma unroll
+              for (int e = 0; e < 16; ++e) sum[e] += part[e];
+            }
           }
+          acc[i][j] = sum;
         }
-      }
       __syncthreads();
     }
 
-    if (kg == 0) {
+    {
       if (a.splits == 1) {
         epilogue(acc, tc);
       } else {
@@ -872,6 +894,7 @@ void conv3x3_kernel(ConvArgs a) {
           for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+              if (!mine(i, j)) continue;
               const i32x4 v = {__float_as_int(acc[i][j][4 * q]), __float_as_int(acc[i][j][4 * q + 1]),
                                __float_as_int(acc[i][j][4 * q + 2]), __float_as_int(acc[i][j][4 * q + 3])};
               __builtin_amdgcn_raw_buffer_store_b128(v, pr, voff + ((i * TN + j) * 4 + q) * 1024, 0,
@@ -897,8 +920,9 @@ void conv3x3_kernel(ConvArgs a) {
                 static_cast<unsigned int>(a.splits - 1);
     __syncthreads();
     if (!*s_last) return;
-    if (kg == 0) {
-      // the tile's partial sums, read back with system-coherent 16-byte loads
+    {
+      // the partial sums of the tiles this wave finishes, read back with
+      // system-coherent 16-byte loads (tiles of other waves left as zeros)
       const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
           a.partials + static_cast<int64_t>(mn) * a.splits * n_chunks * (C::BM * C::BN), 0, -1,
           kRsrcWord3);
@@ -910,6 +934,11 @@ void conv3x3_kernel(ConvArgs a) {
           for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+              if (!mine(i, j)) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) dst[i][j][4 * q + c] = 0.0f;
+                continue;
+              }
               const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
                   pr, voff + ((i * TN + j) * 4 + q) * 1024, 0, kSystemCoherent);
 #pragma unroll
