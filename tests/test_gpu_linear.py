@@ -63,9 +63,13 @@ def test_fused_linear_neuron_module_paths():
     assert (s16 == ref).float().mean().item() >= 0.999
 
 
-@pytest.mark.parametrize("T,R,K,N,splits", [(4, 32, 4096, 32, 0), (6, 8, 512, 64, 1),
-                                            (1, 12, 256, 96, 1), (5, 32, 1024, 32, 4)])
-def test_linear_mean_t_matches_f64(T, R, K, N, splits):
+@pytest.mark.parametrize("T,R,K,N,splits,tile", [(4, 32, 4096, 32, 0, -1), (6, 8, 512, 64, 1, -1),
+                                                 (1, 12, 256, 96, 1, -1), (5, 32, 1024, 32, 4, -1),
+                                                 # K-group tiles whose accumulator tiles are
+                                                 # finished by different groups
+                                                 (4, 32, 4096, 64, 1, 7), (5, 24, 1024, 128, 1, 9),
+                                                 (4, 32, 2048, 96, 2, 41)])
+def test_linear_mean_t_matches_f64(T, R, K, N, splits, tile):
     """snnk_linear_mean_t: the time average of x.w^T + b (the classifier head
     read as model(x).mean(0)) within fp32 accumulation error of float64,
     and equal to the mean of linear_preact's own per-step outputs within
@@ -76,15 +80,16 @@ def test_linear_mean_t_matches_f64(T, R, K, N, splits):
     w = (torch.randn(N, K, generator=g) * K ** -0.5).to(torch.bfloat16)
     b = torch.randn(N, generator=g) * 0.1
     xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
-    m = linear_mean_t(xd, wd, bd, splits=splits).cpu().double()
+    kw = dict(splits=splits, tile_hint=tile)
+    m = linear_mean_t(xd, wd, bd, **kw).cpu().double()
     ref = (x.double() @ w.double().t() + b.double()).mean(0)
     absref = (x.double() @ w.double().abs().t()).mean(0) + b.double().abs()
     assert m.shape == (R, N)
     assert torch.all((m - ref).abs() <= 3e-5 * absref + 1e-6)
-    per_step = linear_preact(xd, wd, bd, splits=splits).cpu().double().mean(0)
+    per_step = linear_preact(xd, wd, bd, **kw).cpu().double().mean(0)
     assert torch.allclose(m, per_step, rtol=1e-6, atol=1e-6)
     # repeated calls are bit-identical (fixed summation order)
-    assert torch.equal(linear_mean_t(xd, wd, bd, splits=splits).cpu().double(), m)
+    assert torch.equal(linear_mean_t(xd, wd, bd, **kw).cpu().double(), m)
 
 
 @pytest.mark.parametrize("T,R,K,N,splits", [(4, 32, 2048, 2048, 0), (5, 8, 256, 128, 1),
