@@ -499,7 +499,8 @@ def _vgg_layer_steps(eng, image, T):
     activations the engine itself produced, in the engine's formats (packed
     words between conv layers, bf16 out of the pooled 2x2 layer)."""
     from snnk.kernels.conv import conv3x3_image_lif
-    from snnk.kernels.linear import linear_bias_lif, linear_bias_lif_act, linear_mean_t
+    from snnk.kernels.linear import (linear_bias_lif, linear_bias_lif_act, linear_mean_t,
+                                     linear_mean_t_bits)
 
     B = image.shape[0]
     lif = eng._lif()
@@ -533,13 +534,19 @@ def _vgg_layer_steps(eng, image, T):
     if R != B:
         f = torch.nn.functional.pad(f, (0, 0, 0, R - B))
     f = f.contiguous()
+    n_cls = eng.num_classes
     for nm, w, b, last in (("FC1", eng.fc1_w, eng.fc1_b, False),
                            ("FC2", eng.fc2_w, eng.fc2_b, False),
                            ("FC3", eng.fc3_w, eng.fc3_b, True)):
         fin = f
-        # as the engine: FC1 writes packed words when spikes travel packed
-        ob = bits and nm == "FC1"
-        if last:
+        # as the engine's mean-over-T forward: FC1 and FC2 write packed words
+        # when spikes travel packed, and the head reads them
+        ob = bits
+        if last and fin.dtype == torch.int32:
+            w, b = w[:n_cls], b[:n_cls]
+            f = linear_mean_t_bits(fin, w, b)
+            fn = (lambda a=fin, w=w, b=b, o=torch.empty_like(f): linear_mean_t_bits(a, w, b, out=o))
+        elif last:
             f = linear_mean_t(fin, w, b)
             fn = (lambda a=fin, w=w, b=b, o=torch.empty_like(f): linear_mean_t(a, w, b, out=o))
         elif fin.dtype == torch.int32 or ob:
@@ -562,7 +569,8 @@ def _vgg_teacher_forced(eng, params, img_cpu, T, dev):
     (packed words into the conv layers); FC3: max |logit error|."""
     from snnk.kernels.binary import pack_bits
     from snnk.kernels.conv import conv3x3_image_lif, to_nhwc_bf16
-    from snnk.kernels.linear import linear_bias_lif, linear_bias_lif_act, linear_preact
+    from snnk.kernels.linear import (linear_bias_lif, linear_bias_lif_act, linear_mean_t_bits,
+                                     linear_preact)
     from oracle import vgg as ov
 
     B = img_cpu.shape[0]
@@ -591,11 +599,12 @@ def _vgg_teacher_forced(eng, params, img_cpu, T, dev):
             first = len(fcs) == 1
             xp = torch.nn.functional.pad(r["input"], (0, 0, 0, R - B))
             xp = xp.to(dev, torch.bfloat16).contiguous()
-            # the engine's formats: FC1 bf16 in, packed words out; FC2 packed in
+            # the engine's formats: FC1 bf16 in, FC2 packed words in, both
+            # packed words out
             if eng.bits_between_layers:
                 xin = xp if first else pack_bits(xp, dim=-1)
-                y = linear_bias_lif_act(xin, w, b, out_bits=first, **lif)
-                y = (_unpack_words(y, w.shape[0]) if first else y.float())[:, :B]
+                y = linear_bias_lif_act(xin, w, b, out_bits=True, **lif)
+                y = _unpack_words(y, w.shape[0])[:, :B]
             else:
                 y = linear_bias_lif(xp, w, b, **lif)[:, :B]
             out.append({"layer": "FC%d" % (3 - len(fcs) - 1),
@@ -603,9 +612,17 @@ def _vgg_teacher_forced(eng, params, img_cpu, T, dev):
                         "rate": r["output"].mean().item()})
             continue
         else:
+            # the engine's mean-over-T head on packed words (or, with bf16
+            # between layers, the per-step logits), against the oracle
             xp = torch.nn.functional.pad(r["input"], (0, 0, 0, R - B))
-            y = linear_preact(xp.to(dev, torch.bfloat16).contiguous(), eng.fc3_w, eng.fc3_b)
-            err = (y.cpu()[:, :B, :eng.num_classes] - r["output"]).abs().max().item()
+            xp = xp.to(dev, torch.bfloat16).contiguous()
+            n = eng.num_classes
+            if eng.bits_between_layers:
+                y = linear_mean_t_bits(pack_bits(xp, dim=-1), eng.fc3_w[:n], eng.fc3_b[:n])
+                err = (y.cpu()[:B] - r["output"].mean(0)).abs().max().item()
+            else:
+                y = linear_preact(xp, eng.fc3_w, eng.fc3_b)
+                err = (y.cpu()[:, :B, :n] - r["output"]).abs().max().item()
             out.append({"layer": "FC3", "max_abs_logit_err": err,
                         "logit_scale": r["output"].abs().max().item()})
             continue

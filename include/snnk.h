@@ -347,6 +347,22 @@ int snnk_linear_mean_t(const uint16_t* x, const uint16_t* w, const float* bias, 
                        int32_t splits, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * The same head on packed spike words x [T][R][K/32] (bit k%32 of word k/32,
+ * K % 32 == 0) for few outputs (N <= 64, SNNK_EUNSUPPORTED otherwise):
+ * out[r][n] = (sum_k c[r][k] * w[n][k]) / T + bias[n], with c[r][k] the
+ * spike count of input k over the T steps (the spikes are 0/1, so the T dot
+ * products of the time average are one).  w [N][K] bf16, 16-byte aligned;
+ * fp32 sums, reduced in a fixed order.  No workspace.
+ *
+ * Replaces, like snnk_linear_mean_t, the VGG classifier's last nn.Linear and
+ *   the mean over T (snn_compiler/zoo/vgg.py:107-114,
+ *   examples/vgg16_snn/benchmark_inference.py:68) when the layer before it
+ *   writes packed spikes.
+ */
+int snnk_linear_mean_t_bits(const uint32_t* x, const uint16_t* w, const float* bias, float* out,
+                            int64_t T, int64_t R, int64_t K, int64_t N, void* stream);
+
+/*
  * Spike self-attention core: per (batch, head) and step t, integer
  * S = Q K^T and O = S V on int8 MFMA over {0,1} spikes (no softmax), then
  * a multi-step LIF on in_scale * O (in_scale = scale / tau for a LIF with

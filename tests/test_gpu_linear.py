@@ -4,6 +4,7 @@ import torch
 import torch.nn.functional as F
 
 import snnk.nn as snn
+from snnk._abi import SnnkError
 from oracle import neurons as on
 from snnk.kernels.linear import linear_bias_lif, linear_preact
 
@@ -157,3 +158,47 @@ def test_dense_small_map_conv_matches_conv_kernel(pool, B, Cin, Cout):
     else:
         spk = spk.view(T, B, H, W, Cout)
     assert torch.equal(dense, spk)
+
+@pytest.mark.parametrize("T,R,K,N,with_bias", [(4, 32, 4096, 10, True), (1, 5, 64, 1, True),
+                                               (6, 12, 1024, 64, True), (3, 8, 8192, 33, False),
+                                               (5, 3, 96, 16, True)])
+def test_linear_mean_t_bits_matches_f64(T, R, K, N, with_bias):
+    """snnk_linear_mean_t_bits: spike counts over T dotted with w, / T + bias,
+    on packed words: within fp32 accumulation error of the float64 time
+    average, close to the bf16-input head, and bit-identical on repeats."""
+    from snnk.kernels.binary import pack_bits
+    from snnk.kernels.linear import linear_mean_t, linear_mean_t_bits
+    g = torch.Generator().manual_seed(T * 100 + K + N)
+    x = (torch.rand(T, R, K, generator=g) < 0.3).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * K ** -0.5).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.1 if with_bias else None
+    xd, wd = x.to(DEV), w.to(DEV)
+    bd = b.to(DEV) if with_bias else None
+    xp = pack_bits(xd, dim=-1)
+    m = linear_mean_t_bits(xp, wd, bd).cpu().double()
+    ref = (x.double() @ w.double().t()).mean(0)
+    absref = (x.double() @ w.double().abs().t()).mean(0)
+    if with_bias:
+        ref = ref + b.double()
+        absref = absref + b.double().abs()
+    assert m.shape == (R, N)
+    assert torch.all((m - ref).abs() <= 3e-5 * absref + 1e-6)
+    assert torch.equal(linear_mean_t_bits(xp, wd, bd).cpu().double(), m)
+    if N % 32 == 0 or N <= 32:
+        wp = torch.zeros((N + 31) // 32 * 32, K, dtype=torch.bfloat16, device=DEV)
+        wp[:N] = wd
+        bp = torch.zeros(wp.shape[0], device=DEV)
+        if with_bias:
+            bp[:N] = bd
+        R4 = (R + 3) // 4 * 4
+        xr = torch.nn.functional.pad(xd, (0, 0, 0, R4 - R)).contiguous()
+        mm = linear_mean_t(xr, wp, bp).cpu().double()[:R, :N]
+        assert torch.all((m - mm).abs() <= 3e-5 * absref + 1e-6)
+
+
+def test_linear_mean_t_bits_refuses_wide_heads():
+    from snnk.kernels.binary import pack_bits
+    from snnk.kernels.linear import linear_mean_t_bits
+    xp = pack_bits(torch.zeros(2, 4, 64, dtype=torch.bfloat16, device=DEV), dim=-1)
+    with pytest.raises(SnnkError):
+        linear_mean_t_bits(xp, torch.zeros(65, 64, dtype=torch.bfloat16, device=DEV), None)

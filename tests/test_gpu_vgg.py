@@ -121,14 +121,17 @@ def test_graph_replay_equals_eager():
 
 def test_mean_over_t_head_and_graph():
     """forward(mean_t=True) folds the logits' mean over T into the last
-    layer (what the bench times): equal to forward().mean(0) within fp32
-    rounding, eager and replayed."""
+    layer (what the bench times): with packed spikes between layers the head
+    counts each input's spikes over T and takes one dot product, so it equals
+    forward().mean(0) (T per-step dot products) within the fp32 rounding of
+    the two summation orders; eager and replayed results are identical."""
     eng = _engine(3.0)
     img = _image(32, seed=4).to(DEV)
     full = eng(img)
     m = eng(img, mean_t=True)
     assert m.shape == (32, 10)
-    assert torch.allclose(m, full.mean(0), rtol=1e-6, atol=1e-6)
+    scale = full.abs().max().item()
+    assert torch.allclose(m, full.mean(0), rtol=1e-5, atol=1e-5 * scale)
     for _ in range(2):
         eng(_image(32, seed=9).to(DEV))
         assert torch.equal(eng.run_graph(img, mean_t=True), m)

@@ -140,6 +140,11 @@ PROTOTYPES: dict[str, list] = {
         _p, _i64,              # workspace, workspace_bytes
         _p,                    # stream
     ],
+    "snnk_linear_mean_t_bits": [
+        _p, _p, _p, _p,        # x words, w, bias, out
+        _i64, _i64, _i64, _i64,  # T, R, K, N
+        _p,                    # stream
+    ],
     "snnk_spike_attention": [
         _p, _p, _p,            # q, k, v
         _i64, _i64, _i64,      # q_row, k_row, v_row

@@ -208,3 +208,27 @@ def linear_mean_t(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *
                   T, R, K, N, int(tile_hint), sp, _abi.ptr(ws), 0 if ws is None else ws.numel(),
                   _abi.stream(x.device))
     return out
+def linear_mean_t_bits(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, *,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """x int32 packed spike words [T, R, K // 32], w [N, K] bf16 (N <= 64) ->
+    fp32 [R, N]: the time average of x.w^T + bias, computed as
+    (spike counts over T) . w / T + bias in one pass over K (the spikes are
+    0/1).  The classifier head of :func:`linear_mean_t` for a layer that
+    writes packed spikes."""
+    assert x.is_cuda and x.dtype == torch.int32 and x.ndim == 3 and x.is_contiguous()
+    assert w.dtype == torch.bfloat16 and w.ndim == 2 and w.is_contiguous() and w.device == x.device
+    T, R, KW = x.shape
+    N, K = w.shape
+    assert K == 32 * KW, f"K = {K} against {KW} words"
+    if bias is not None:
+        assert bias.dtype == torch.float32 and bias.shape == (N,) and bias.is_contiguous()
+    if out is None:
+        out = torch.empty(R, N, device=x.device, dtype=torch.float32)
+    else:
+        assert out.shape == (R, N) and out.dtype == torch.float32 and out.is_contiguous()
+    with torch.cuda.device(x.device):
+        _abi.call("snnk_linear_mean_t_bits", x.data_ptr(), w.data_ptr(), _abi.ptr(bias),
+                  out.data_ptr(), T, R, K, N, _abi.stream(x.device))
+    return out
+
+

@@ -11,7 +11,9 @@ forward as fused HIP kernels over NHWC bf16 spikes:
     (snnk_conv3x3_image_lif);
   * every other conv: conv3x3 + folded BN + LIF (+ 2x2 max) in one bf16-MFMA
     kernel (snnk_conv3x3_bn_lif);
-  * FC1, FC2: Linear + bias + LIF in one bf16-MFMA kernel; FC3: Linear + bias.
+  * FC1, FC2: Linear + bias + LIF in one bf16-MFMA kernel; FC3: Linear + bias
+    per step, or (``mean_t``) its mean over T: from FC2's packed words, spike
+    counts over T dotted with the weights (snnk_linear_mean_t_bits).
 It returns ``[T, B, num_classes]`` like the reference; the caller averages
 over T (examples/vgg16_snn/vgg16_test.py:243).  ``capture`` records the
 forward in a HIP graph for a fixed batch.
@@ -30,7 +32,8 @@ from ..nn.modules import (
 from ..passes.fuse import fuse_snn_model
 from ..kernels.conv import conv3x3_image_lif
 from ..kernels.fused import fold_conv_bn
-from ..kernels.linear import linear_bias_lif, linear_bias_lif_act, linear_preact, linear_mean_t
+from ..kernels.linear import (linear_bias_lif, linear_bias_lif_act, linear_mean_t,
+                              linear_mean_t_bits, linear_preact)
 from ..kernels.neurons import neuron_params
 
 VGG16_CFG = [64, 64, "P", 128, 128, "P", 256, 256, 256, "P",
@@ -301,19 +304,23 @@ class FusedVGGSNN(nn.Module):
         if R != B:
             x = F.pad(x, (0, 0, 0, R - B))
         # FC1 takes the features in whichever format the last conv wrote and,
-        # with packed spikes between layers, hands FC2 packed words; FC2 writes
-        # bf16 spikes for FC3 (its mean-over-T head reads bf16)
+        # with packed spikes between layers, hands FC2 packed words.  FC2 hands
+        # the mean-over-T head packed words too (it counts each input's spikes
+        # over T and runs one dot product); the per-step head reads bf16
         bits = self.bits_between_layers
         x = (linear_bias_lif_act(x, self.fc1_w, self.fc1_b, out_bits=bits, **self._lif())
              if x.dtype == torch.int32 or bits
              else linear_bias_lif(x, self.fc1_w, self.fc1_b, **self._lif()))
         if rates is not None:
             rates.append(spike_rate(x[:, :B]))
-        x = (linear_bias_lif_act(x, self.fc2_w, self.fc2_b, out_bits=False, **self._lif())
+        x = (linear_bias_lif_act(x, self.fc2_w, self.fc2_b, out_bits=bits and mean_t, **self._lif())
              if x.dtype == torch.int32 else linear_bias_lif(x, self.fc2_w, self.fc2_b, **self._lif()))
         if rates is not None:
-            rates.append(x[:, :B].float().mean())
+            rates.append(spike_rate(x[:, :B]))
         if mean_t:
+            if x.dtype == torch.int32:
+                n = self.num_classes
+                return linear_mean_t_bits(x, self.fc3_w[:n], self.fc3_b[:n])[:B]
             return linear_mean_t(x, self.fc3_w, self.fc3_b)[:B, :self.num_classes]
         y = linear_preact(x, self.fc3_w, self.fc3_b)
         return y[:, :B, :self.num_classes]
