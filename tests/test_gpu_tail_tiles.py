@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 LIF = dict(decay=0.5, in_scale=0.5, v_threshold=1.0)
 # bf16 ring tiles with the same K groups: 4 -> tile 4 (32x32), 8 -> tile 6, 2 -> tile 13
-SAME_GROUPS = {39: 4, 40: 6, 41: 13}
+SAME_GROUPS = {39: 4, 40: 6, 41: 13, 42: 4}
 
 
 def _pack(s):
@@ -43,6 +43,8 @@ CONV = [  # T, B, Cin, Cout, H, W, pool, tile, splits
     (5, 2, 256, 256, 4, 4, True, 40, 1),     # two 4-step chunks
     (3, 4, 512, 96, 2, 2, False, 39, 2),     # Cout 96, steps past T, split
     (4, 6, 256, 160, 4, 4, False, 41, 3),
+    (4, 8, 256, 256, 4, 4, False, 42, 1),    # 64 x 32 tiles
+    (5, 3, 256, 96, 4, 4, True, 42, 2),      # two chunks, pool, split
 ]
 
 
@@ -69,6 +71,9 @@ LINEAR = [  # T, R, K, N, tile, splits
     (4, 56, 512, 4096, 41, 1),    # FC1 at batch 56
     (4, 56, 2048, 2048, 40, 1),   # L11 as a dense Linear at batch 56
     (6, 20, 1024, 256, 41, 2),    # two chunks, split
+    (4, 32, 4096, 1024, 42, 1),   # FC2's K at batch 32 on 64 x 32 tiles
+    (4, 56, 2048, 2048, 42, 1),   # L11 as a dense Linear at batch 56
+    (5, 20, 1024, 96, 42, 3),     # two chunks, partial tiles, split
 ]
 
 
@@ -96,3 +101,13 @@ def test_tail_tiles_bf16_form_refused():
     for tile in (39, 40):
         with pytest.raises(SnnkError):
             kc.conv3x3_bn_lif_nhwc(x.to(DEV), wp, bd, pool=False, tile_hint=tile, splits=1, **LIF)
+
+
+@pytest.mark.parametrize("pool", [False, True])
+def test_tile_42_packed_equals_its_bf16_form(pool):
+    """Tile 42 (64 x 32, 4 K groups) also runs bf16 input: both give the same spikes."""
+    x, wp, bd = _conv_case(4, 8, 256, 256, 4, 4, seed=42)
+    ref = kc.conv3x3_bn_lif_nhwc(x.to(DEV), wp, bd, pool=pool, tile_hint=42, splits=1, **LIF).cpu()
+    assert 0 < int(ref.float().sum()) < ref.numel()
+    got = kc.conv3x3_bn_lif_act(_pack(x).to(DEV), wp, bd, pool=pool, tile_hint=42, splits=1, **LIF)
+    assert torch.equal(got.cpu(), _pack(ref))

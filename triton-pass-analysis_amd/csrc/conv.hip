@@ -39,7 +39,7 @@
 namespace snnk {
 namespace {
 
-constexpr int kNumTiles = 42;
+constexpr int kNumTiles = 43;
 struct TileShape { int bm, bn; };
 //                                   0          1         2          3         4        5
 constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 128}, {32, 32}, {32, 128},
@@ -52,8 +52,8 @@ constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 
 //   29 - 38: resident weights, packed x only
     {512, 64}, {256, 64}, {512, 32}, {256, 128}, {256, 32}, {256, 64}, {512, 64}, {512, 32},
     {256, 32}, {256, 128},
-//   39         40         41
-    {64, 64}, {64, 64}, {64, 64}};
+//   39         40         41        42
+    {64, 64}, {64, 64}, {64, 64}, {64, 32}};
 
 // Tile shape by problem size (rows = output rows of one 4-step chunk, K =
 // 9*Cin or the Linear depth): big tiles while M fills 256 CUs, split-K wave
@@ -163,13 +163,14 @@ bool auto_cfg_packed(const ConvArgs& a, bool taps9, int* cfg, int* splits) {
     // K = 384, 1152 columns: 17.8 us with 128 x 64 tiles, 21.9 with 128 x 128)
     if (rows >= 8192 && K <= 512) { *cfg = a.Cout > 512 ? 10 : 9; return true; }
     if (rows <= 64 || rows > 256) return false;
-    // FC2 (K = 4096): 32x32 tiles with 4 K groups at batch 32 (13.5 us against
-    // 15.2 with 32x64 tiles and 2 splits), 64x64 with 4 groups at batch 56
-    // (16.6 against 21.3); the dense 2x2 layers (K = 2048) at batch 56: 32x32
-    // tiles, 4 groups, no split (9.1 us against 11.8); FC1 (K = 512, 4096
-    // columns) at batch 56: 64x64 tiles, 2 groups (7.4 against 8.0)
-    if (K >= 4096) { *cfg = rows <= 128 ? 4 : 39; return true; }
-    if (K >= 2048) { if (rows <= 128) return false; *cfg = 4; return true; }
+    // FC2 (K = 4096): 64x32 tiles with 4 K groups at batch 32 (12.2 us
+    // against 14.3 with 32x32 tiles), 64x64 with 4 groups at batch 56 (14.9
+    // against 17.4 with 64x32); the dense 2x2 layers (K = 2048) at batch 56:
+    // 64x32 tiles, 4 groups, no split (8.4 us against 9.4 with 32x32); FC1
+    // (K = 512, 4096 columns) at batch 56: 64x64 tiles, 2 groups (7.4
+    // against 8.0)
+    if (K >= 4096) { *cfg = rows <= 128 ? 42 : 39; return true; }
+    if (K >= 2048) { if (rows <= 128) return false; *cfg = 42; return true; }
     if (K <= 512) { *cfg = rows <= 128 ? 4 : a.Cout > 512 ? 41 : 7; return true; }
     return false;
   }

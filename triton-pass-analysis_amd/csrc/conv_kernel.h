@@ -1064,6 +1064,9 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
     case 39: return launch_cfg<2, 1, 1, 2, 4, 3, POOL, MODE, TAPS, PK>(a, s);   // 64 x 64 split-K 4
     case 40: return launch_cfg<2, 1, 1, 2, 8, 2, POOL, MODE, TAPS, PK>(a, s);   // 64 x 64 split-K 8
     case 41: return launch_cfg<2, 1, 1, 2, 2, 4, POOL, MODE, TAPS, PK>(a, s);   // 64 x 64 split-K 2
+    // 64 x 32 with K over 4 wave groups: the FC layers over 128-224 rows,
+    // each weight byte read by half as many row tiles as with 32-row tiles
+    case 42: return launch_cfg<2, 1, 1, 1, 4, 3, POOL, MODE, TAPS, PK>(a, s);   // 64 x 32 split-K 4
     default: return SNNK_EINVAL;
   }
 }
