@@ -161,11 +161,11 @@ int snnk_binary_gemm(const uint32_t* A, const uint32_t* B, void* C, int32_t c_dt
  *          (no LIF, pool must be 0): for numerical checks
  * LIF: v = decay*v + in_scale*(conv + bias); spike v >= v_threshold;
  *      hard reset to v_reset or soft reset (v -= v_threshold); state starts at 0.
- * tile_hint: -1 picks the tile shape from the problem size; 0..42 force one
+ * tile_hint: -1 picks the tile shape from the problem size; 0..43 force one
  *          (29..38 keep the block's weights resident in LDS and take packed
  *          spike input only, Cin % 64 == 0; 39 and 40, 64x64 tiles with K over
- *          4 and 8 wave groups, take packed input only: SNNK_EUNSUPPORTED
- *          otherwise).
+ *          4 and 8 wave groups, and 43, 128x64 with 4 groups, take packed
+ *          input only: SNNK_EUNSUPPORTED otherwise).
  */
 int snnk_conv3x3_bn_lif(const uint16_t* x, const uint16_t* w, const float* bias,
                         uint16_t* spikes_out, float* preact_out,

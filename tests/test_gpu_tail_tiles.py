@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 LIF = dict(decay=0.5, in_scale=0.5, v_threshold=1.0)
 # bf16 ring tiles with the same K groups: 4 -> tile 4 (32x32), 8 -> tile 6, 2 -> tile 13
-SAME_GROUPS = {39: 4, 40: 6, 41: 13, 42: 4}
+SAME_GROUPS = {39: 4, 40: 6, 41: 13, 42: 4, 43: 4}
 
 
 def _pack(s):
@@ -45,6 +45,9 @@ CONV = [  # T, B, Cin, Cout, H, W, pool, tile, splits
     (4, 6, 256, 160, 4, 4, False, 41, 3),
     (4, 8, 256, 256, 4, 4, False, 42, 1),    # 64 x 32 tiles
     (5, 3, 256, 96, 4, 4, True, 42, 2),      # two chunks, pool, split
+    (4, 14, 512, 512, 4, 4, False, 43, 1),   # L9 at batch 14 on 128 x 64 tiles
+    (4, 10, 512, 512, 4, 4, True, 43, 1),    # L10, rows not a multiple of 128
+    (5, 3, 256, 96, 4, 4, False, 43, 2),     # two chunks, Cout 96, split
 ]
 
 
@@ -74,6 +77,7 @@ LINEAR = [  # T, R, K, N, tile, splits
     (4, 32, 4096, 1024, 42, 1),   # FC2's K at batch 32 on 64 x 32 tiles
     (4, 56, 2048, 2048, 42, 1),   # L11 as a dense Linear at batch 56
     (5, 20, 1024, 96, 42, 3),     # two chunks, partial tiles, split
+    (4, 56, 4096, 512, 43, 1),    # 128 x 64 tiles on a Linear
 ]
 
 
@@ -96,9 +100,9 @@ def test_tail_tile_linear_equals_bf16_tile_with_same_k_groups(T, R, K, N, tile, 
 
 
 def test_tail_tiles_bf16_form_refused():
-    """Tiles 39 and 40 need more LDS than a CU has with bf16 A: refused, not launched."""
+    """Tiles 39, 40 and 43 need more LDS than a CU has with bf16 A: refused, not launched."""
     x, wp, bd = _conv_case(4, 2, 256, 128, 4, 4, seed=3)
-    for tile in (39, 40):
+    for tile in (39, 40, 43):
         with pytest.raises(SnnkError):
             kc.conv3x3_bn_lif_nhwc(x.to(DEV), wp, bd, pool=False, tile_hint=tile, splits=1, **LIF)
 

@@ -39,7 +39,7 @@
 namespace snnk {
 namespace {
 
-constexpr int kNumTiles = 43;
+constexpr int kNumTiles = 44;
 struct TileShape { int bm, bn; };
 //                                   0          1         2          3         4        5
 constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 128}, {32, 32}, {32, 128},
@@ -52,8 +52,8 @@ constexpr TileShape kTile[kNumTiles] = {{128, 256}, {256, 64}, {128, 128}, {64, 
 //   29 - 38: resident weights, packed x only
     {512, 64}, {256, 64}, {512, 32}, {256, 128}, {256, 32}, {256, 64}, {512, 64}, {512, 32},
     {256, 32}, {256, 128},
-//   39         40         41        42
-    {64, 64}, {64, 64}, {64, 64}, {64, 32}};
+//   39         40         41        42         43
+    {64, 64}, {64, 64}, {64, 64}, {64, 32}, {128, 64}};
 
 // Tile shape by problem size (rows = output rows of one 4-step chunk, K =
 // 9*Cin or the Linear depth): big tiles while M fills 256 CUs, split-K wave
@@ -197,10 +197,11 @@ bool auto_cfg_packed(const ConvArgs& a, bool taps9, int* cfg, int* splits) {
   if (rows >= 2048) {                             // L8 - L10
     if (K <= 1152) { *cfg = 4; return true; }
     // 64x64 tiles, K over 4 wave groups at batch 32 (2048 rows: L9 18.5 us
-    // against 20.9 with 32x64 tiles) and over 2 at batch 56 (L10 26.3 against
-    // 29.5 with 128x64 tiles and 2 splits): each weight byte is re-read by
-    // half as many row tiles as with 32-row tiles
-    *cfg = rows <= 2048 ? 39 : 41;
+    // against 20.9 with 32x64 tiles): each weight byte is re-read by half as
+    // many row tiles as with 32-row tiles.  At batch 56 (3584 rows) 128x64
+    // tiles with 4 K groups and 16 waves, one round of 224 blocks (L9 23.3 us
+    // against 26.1 with 64x64 tiles and 2 groups, L10 22.5 against 26.0)
+    *cfg = rows <= 2048 ? 39 : 43;
     return true;
   }
   return false;

@@ -1067,6 +1067,10 @@ int dispatch(const ConvArgs& a0, const Plan& p, void* workspace, hipStream_t s) 
     // 64 x 32 with K over 4 wave groups: the FC layers over 128-224 rows,
     // each weight byte read by half as many row tiles as with 32-row tiles
     case 42: return launch_cfg<2, 1, 1, 1, 4, 3, POOL, MODE, TAPS, PK>(a, s);   // 64 x 32 split-K 4
+    // 128 x 64 with K over 4 wave groups, 16 waves: the 4x4 layers at batch
+    // 56 (3584 rows: 224 tiles, one round of blocks instead of 1.75 rounds
+    // of 64 x 64 tiles)
+    case 43: return launch_cfg<4, 1, 1, 2, 4, 3, POOL, MODE, TAPS, PK>(a, s);   // 128 x 64 split-K 4
     default: return SNNK_EINVAL;
   }
 }
