@@ -33,6 +33,7 @@
 // lane's source offsets are rebuilt only when the stage's tap changes.
 #pragma once
 
+#include <algorithm>
 #include <cstddef>
 #include <type_traits>
 
@@ -160,6 +161,8 @@ struct Cfg {
   static constexpr int kAStageBytes = KSPLIT * BM * kARowBytes;  // B follows A in a stage
   static constexpr int kStageBytes = kAStageBytes + KSPLIT * BN * kRowBytes;
   static constexpr int kBuf = NBUF;  // ring of operand stages in LDS
+  // (resident weights: the most a block may take; the launch sizes it to
+  // the block's K stages)
   static constexpr int kLdsBytes = kRes ? kResBytes : kBuf * kStageBytes;
   // K-group sums: a slot per (group, wave, tile) for the tiles another
   // group finishes
@@ -207,7 +210,16 @@ __global__ __launch_bounds__(64 * WM * WN * KSPLIT)
 void conv3x3_kernel(ConvArgs a) {
   using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF, PK>;
   static_assert(C::kFits, "LDS ring must fit 160 KB");
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::kSmem];
+  unsigned char* smem;
+  if constexpr (C::kRes) {
+    // resident weights: LDS sized at launch to the block's K stages (BN rows
+    // of 128 bytes each), so that a short-K layer fits several blocks per CU
+    extern __shared__ __attribute__((aligned(1024))) unsigned char smem_res[];
+    smem = smem_res;
+  } else {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem_ring[C::kSmem];
+    smem = smem_ring;
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -979,8 +991,12 @@ int launch_cfg(const ConvArgs& a, hipStream_t stream) {
       return SNNK_EUNSUPPORTED;
     const int64_t per_xcd = (static_cast<int64_t>(a.tiles_m) * a.tiles_n * a.splits + 7) / 8;
     if (per_xcd * 8 > 0x7FFFFFFFll) return SNNK_EUNSUPPORTED;
+    // resident weights: the block's K stages of BN rows (at least the word
+    // of the split-K ticket result)
+    const unsigned dyn_lds =
+        C::kRes ? static_cast<unsigned>(std::max(4, a.stages_per_split * C::BN * kRowBytes)) : 0u;
     hipLaunchKernelGGL((conv3x3_kernel<WM, WN, TM, TN, KSPLIT, NBUF, POOL, MODE, TAPS, PK>),
-                       dim3(static_cast<unsigned>(per_xcd * 8)), dim3(C::kThreads), 0, stream, a);
+                       dim3(static_cast<unsigned>(per_xcd * 8)), dim3(C::kThreads), dyn_lds, stream, a);
     return launch_status();
   }
 }
