@@ -141,11 +141,16 @@ bool auto_cfg_packed(const ConvArgs& a, bool taps9, int* cfg, int* splits) {
   // (tiles / whole waves of 256 blocks), weighted 0.55 for 32-column tiles,
   // whose waves expand each spike fragment for one MFMA instead of two (VGG
   // L2 at batch 56: 256x32 tiles fill 1.0 and take 42 us, 512x64 fill 0.875
-  // and take 25); ties to 64 columns, then 512 rows.  Below half a wave of
-  // blocks, or below 8192 rows (batch 1), the streamed tiles are faster.
+  // and take 25); ties to 64 columns, then 512 rows, or 256 rows where two
+  // blocks' weights fit a CU's LDS (VGG L2 at batch 56: 23.0 us with 256 x 64
+  // tiles, two blocks per CU, against 24.6 with 512 x 64).  Below half a wave
+  // of blocks, or below 8192 rows (batch 1), the streamed tiles are faster.
   if (taps9 && rows >= 8192 && a.Cin % kKS == 0) {
     struct Res { int cfg, bm, bn; };
-    constexpr Res kRes[] = {{35, 512, 64}, {34, 256, 64}, {31, 512, 32}, {37, 256, 32}};
+    const bool two_per_cu = K * 64 * 2 * 2 <= kResBytes;
+    const Res kRes[] = {two_per_cu ? Res{34, 256, 64} : Res{35, 512, 64},
+                        two_per_cu ? Res{35, 512, 64} : Res{34, 256, 64},
+                        {31, 512, 32}, {37, 256, 32}};
     int best = -1;
     double best_score = 0.0, best_fill = 0.0;
     for (const Res& r : kRes) {

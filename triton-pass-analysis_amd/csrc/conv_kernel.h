@@ -204,9 +204,22 @@ __device__ __forceinline__ int tap_dy(int tap) { return TAPS == 9 ? tap / 3 - 1 
 template <int TAPS>
 __device__ __forceinline__ int tap_dx(int tap) { return TAPS == 9 ? tap % 3 - 1 : 0; }
 
+// Waves per SIMD a tile's registers must leave room for.  The packed Linear
+// 128 x 64 tile serves the short-K projections over many rows (the SSA
+// block's QKV: 1152 blocks over 8192 rows, K = 384): unbounded it takes 152
+// registers, 3 waves per SIMD, so only 3 of its 4.5 blocks per CU are
+// resident at once; bounded to 96 (5 waves, 28 bytes of spills) all are
+// (16.4 us against 18.0; 4 waves, 110 registers: 16.9).
+template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, int TAPS, bool PK>
+constexpr int min_waves_per_simd() {
+  return WM == 4 && WN == 1 && TM == 1 && TN == 2 && KSPLIT == 1 && NBUF == 3 && TAPS == 1 && PK
+             ? 5 : 1;
+}
+
 template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int MODE, int TAPS,
           bool PK>
-__global__ __launch_bounds__(64 * WM * WN * KSPLIT)
+__global__ __launch_bounds__(64 * WM * WN * KSPLIT,
+                             (min_waves_per_simd<WM, WN, TM, TN, KSPLIT, NBUF, TAPS, PK>()))
 void conv3x3_kernel(ConvArgs a) {
   using C = Cfg<WM, WN, TM, TN, KSPLIT, NBUF, PK>;
   static_assert(C::kFits, "LDS ring must fit 160 KB");
