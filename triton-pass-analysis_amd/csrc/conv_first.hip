@@ -67,7 +67,9 @@ __global__ __launch_bounds__(256) void conv_image_lif_kernel(
   const int y = r / W, x = r - y * W;
 
   // image taps of one channel chunk: rows y-1..y+1, columns x-1..x+P
-  // (zero outside the image or past Cin)
+  // (zero outside the image or past Cin).  Every read goes to the tap's
+  // position clamped into the image (and channel 0 past Cin), so it is in
+  // bounds and needs no branch; the select then zeroes the taps outside.
   float xin[CC][3][P + 2];
   auto load_chunk = [&](int c0) {
 #pragma unroll
@@ -75,13 +77,18 @@ __global__ __launch_bounds__(256) void conv_image_lif_kernel(
       const int c = c0 + cc;
       const float* ip = img + (static_cast<int64_t>(b) * Cin + (c < Cin ? c : 0)) * HW;
 #pragma unroll
-      for (int dy = 0; dy < 3; ++dy)
+      for (int dy = 0; dy < 3; ++dy) {
+        const int ys = y + dy - 1;
+        const int yc = ys < 0 ? 0 : ys >= H ? H - 1 : ys;
 #pragma unroll
         for (int dx = 0; dx < P + 2; ++dx) {
-          const int ys = y + dy - 1, xs = x + dx - 1;
+          const int xs = x + dx - 1;
+          const int xc = xs < 0 ? 0 : xs >= W ? W - 1 : xs;
           const bool in = live && c < Cin && ys >= 0 && ys < H && xs >= 0 && xs < W;
-          xin[cc][dy][dx] = in ? ip[ys * W + xs] : 0.0f;
+          const float v = ip[yc * W + xc];
+          xin[cc][dy][dx] = in ? v : 0.0f;
         }
+      }
     }
   };
   load_chunk(0);
