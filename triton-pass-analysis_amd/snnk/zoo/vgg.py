@@ -265,7 +265,9 @@ class FusedVGGSNN(nn.Module):
     def features_nhwc(self, image: torch.Tensor, rates: list | None = None) -> torch.Tensor:
         """image [B, 3, H, W] fp32 -> spikes of the last conv block, channels
         last: bf16 ``[T, B, H, W, C]`` or (``bits_between_layers``) int32 packed
-        words ``[T, B, H, W, C // 32]``.  Between conv layers the spikes travel
+        words ``[T, B, H, W, C // 32]``; when the last maps are at most 2x2 and
+        B is not a multiple of 4, B is padded to one (zero rows after the
+        first B).  Between conv layers the spikes travel
         as packed words (16x fewer bytes than bf16) when ``bits_between_layers``
         is set.  ``rates`` (optional list) receives every layer's mean firing rate."""
         # packed from the first layer on, unless a pool follows it directly
@@ -277,10 +279,18 @@ class FusedVGGSNN(nn.Module):
         if self.pool0:
             T, B, H, W, C = x.shape
             x = x.view(T, B, H // 2, 2, W // 2, 2, C).amax(dim=(3, 5)).contiguous()
+        B = x.shape[1]
         for conv in self.convs:
+            H, W = x.shape[2:4]
+            if H <= 2 and W <= 2 and x.shape[1] % 4 != 0:
+                # layers on a map of at most 2x2 run as dense Linear layers
+                # over whole quads of rows: the batch is padded with zero
+                # spikes to a multiple of 4 here (its extra rows are dropped
+                # after the classifier; the classifier would pad it anyway)
+                x = F.pad(x, (0, 0, 0, 0, 0, 0, 0, (B + 3) // 4 * 4 - B))
             x = conv.forward_nhwc(x, out_bits=self.bits_between_layers)
             if rates is not None:
-                rates.append(spike_rate(x))
+                rates.append(spike_rate(x[:, :B]))
         return x
 
     def forward(self, image: torch.Tensor, rates: list | None = None,
@@ -299,10 +309,11 @@ class FusedVGGSNN(nn.Module):
             image = image[0]
         image = image.float().contiguous()
         T, B = self.T, image.shape[0]
-        x = self.features_nhwc(image, rates).reshape(T, B, -1)
+        x = self.features_nhwc(image, rates)
+        x = x.reshape(T, x.shape[1], -1)  # B rows, or B padded to a multiple of 4
         R = (B + 3) // 4 * 4
-        if R != B:
-            x = F.pad(x, (0, 0, 0, R - B))
+        if x.shape[1] != R:
+            x = F.pad(x, (0, 0, 0, R - x.shape[1]))
         # FC1 takes the features in whichever format the last conv wrote and,
         # with packed spikes between layers, hands FC2 packed words.  FC2 hands
         # the mean-over-T head packed words too (it counts each input's spikes
