@@ -208,12 +208,13 @@ __device__ __forceinline__ int tap_dx(int tap) { return TAPS == 9 ? tap % 3 - 1 
 // 128 x 64 tile serves the short-K projections over many rows (the SSA
 // block's QKV: 1152 blocks over 8192 rows, K = 384): unbounded it takes 152
 // registers, 3 waves per SIMD, so only 3 of its 4.5 blocks per CU are
-// resident at once; bounded to 96 (5 waves, 28 bytes of spills) all are
-// (16.4 us against 18.0; 4 waves, 110 registers: 16.9).
+// resident at once; bounded to 4 waves it fits 110 registers without spills
+// (16.9 us against 18.0).  A bound of 5 waves (96 registers) ran 16.4 us but
+// spilled 28 bytes per lane, 7 MB of scratch writes per launch.
 template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, int TAPS, bool PK>
 constexpr int min_waves_per_simd() {
   return WM == 4 && WN == 1 && TM == 1 && TN == 2 && KSPLIT == 1 && NBUF == 3 && TAPS == 1 && PK
-             ? 5 : 1;
+             ? 4 : 1;
 }
 
 template <int WM, int WN, int TM, int TN, int KSPLIT, int NBUF, bool POOL, int MODE, int TAPS,
