@@ -35,47 +35,61 @@ __global__ __launch_bounds__(kHeadThreads) void head_mean_bits_kernel(
 
   for (int h = tid; h < 2 * KW; h += kHeadThreads) {
     const int j = h >> 1, sh = (h & 1) * 16;
+    // 16 bf16 weights per output, two 16-byte loads (K % 32 == 0 keeps them
+    // aligned); rows in batches of 8, a batch's loads issued before its
+    // products (rows past N repeat row N - 1; their sums are never read).
+    // The first two batches are loaded before the spike words are counted,
+    // so that the memory round trips overlap; later batches reuse the two
+    // register slots.
+    const uint16_t* wk = w + 16 * h;
+    u32x4 wv[2][8][2];
+    auto load_w = [&](int slot, int n0) __attribute__((always_inline)) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t row = n0 + e < N ? n0 + e : N - 1;
+        wv[slot][e][0] = *reinterpret_cast<const u32x4*>(wk + row * K);
+        wv[slot][e][1] = *reinterpret_cast<const u32x4*>(wk + row * K + 8);
+      }
+    };
+    load_w(0, 0);
+    if (N > 8) load_w(1, 8);
     // spike count of each of the 16 inputs over the T steps; the words of
-    // four steps are loaded before they are counted
+    // four steps are loaded (from step T - 1 for steps past the last, then
+    // zeroed: no branch, no wait between the loads) before they are counted
     float c[16];
 #pragma unroll
     for (int b = 0; b < 16; ++b) c[b] = 0.0f;
     for (int t0 = 0; t0 < T; t0 += 4) {
       uint32_t wd[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        wd[u] = t0 + u < T ? x[(static_cast<int64_t>(t0 + u) * R + r) * KW + j] >> sh : 0u;
+      for (int u = 0; u < 4; ++u) {
+        const int t = t0 + u < T ? t0 + u : T - 1;
+        wd[u] = x[(static_cast<int64_t>(t) * R + r) * KW + j] >> sh;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) wd[u] = t0 + u < T ? wd[u] : 0u;
 #pragma unroll
       for (int u = 0; u < 4; ++u)
 #pragma unroll
         for (int b = 0; b < 16; ++b) c[b] += static_cast<float>((wd[u] >> b) & 1u);
     }
-    // 16 bf16 weights per output, two 16-byte loads (K % 32 == 0 keeps them
-    // aligned); rows in batches of 8, a batch's loads issued before its
-    // products (rows past N repeat row N - 1; their sums are never read)
-    const uint16_t* wk = w + 16 * h;
 #pragma unroll
     for (int n0 = 0; n0 < NMAX; n0 += 8) {
       if (n0 >= N) break;
-      u32x4 wv[8][2];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int64_t row = n0 + e < N ? n0 + e : N - 1;
-        wv[e][0] = *reinterpret_cast<const u32x4*>(wk + row * K);
-        wv[e][1] = *reinterpret_cast<const u32x4*>(wk + row * K + 8);
-      }
+      const int slot = (n0 >> 3) & 1;
+      if (n0 >= 16) load_w(slot, n0);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         float s = acc[n0 + e];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          s = __builtin_fmaf(c[2 * q], __uint_as_float(wv[e][0][q] << 16), s);
-          s = __builtin_fmaf(c[2 * q + 1], __uint_as_float(wv[e][0][q] & 0xFFFF0000u), s);
+          s = __builtin_fmaf(c[2 * q], __uint_as_float(wv[slot][e][0][q] << 16), s);
+          s = __builtin_fmaf(c[2 * q + 1], __uint_as_float(wv[slot][e][0][q] & 0xFFFF0000u), s);
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          s = __builtin_fmaf(c[8 + 2 * q], __uint_as_float(wv[e][1][q] << 16), s);
-          s = __builtin_fmaf(c[9 + 2 * q], __uint_as_float(wv[e][1][q] & 0xFFFF0000u), s);
+          s = __builtin_fmaf(c[8 + 2 * q], __uint_as_float(wv[slot][e][1][q] << 16), s);
+          s = __builtin_fmaf(c[9 + 2 * q], __uint_as_float(wv[slot][e][1][q] & 0xFFFF0000u), s);
         }
         acc[n0 + e] = s;
       }
