@@ -137,6 +137,33 @@ def test_image_layer_run_lengths(B):
     assert 0.01 < got.mean().item() < 0.99
 
 
+@pytest.mark.parametrize("B,Cin,H,W,Cout", [(2, 1, 1, 1, 32), (1, 2, 2, 1, 32), (3, 4, 5, 7, 64),
+                                             (2, 5, 3, 6, 32), (4, 6, 9, 3, 96), (2, 3, 1, 8, 64)])
+def test_image_layer_borders_and_channel_chunks(B, Cin, H, W, Cout):
+    """Maps of 1-9 pixels a side (every tap of a 1x1 image lies outside it),
+    channel chunks of 4 (Cin % 3 != 0) and of 3, Cin short of a whole chunk
+    (channels past Cin read as zeros): spikes match the fp64 conv + LIF away
+    from the threshold, and the packed words are the bf16 spikes packed."""
+    g = torch.Generator().manual_seed(100 + Cin * 7 + H)
+    img = torch.randn(B, Cin, H, W, generator=g)
+    w = torch.randn(Cout, Cin, 3, 3, generator=g) * (2.0 / (9 * Cin)) ** 0.5 * 2
+    b = torch.randn(Cout, generator=g) * 0.1
+    T = 4
+    spk = kc.conv3x3_image_lif(img.to(DEV), w.to(DEV), b.to(DEV), T, decay=0.5,
+                               in_scale=0.5, v_threshold=1.0)
+    y = F.conv2d(img.double(), w.double(), b.double(), padding=1).float()
+    yt = y.unsqueeze(0).expand(T, *y.shape).contiguous()
+    ref, _, _ = on.lif_multistep(yt, neuron="lif")
+    hs = of.membrane_trace(yt)
+    got = spk.cpu().float().permute(0, 1, 4, 2, 3)
+    near = torch.cummax(((hs - 1.0).abs() < 1e-5).int(), dim=0).values.bool()
+    assert not torch.any((got != ref) & ~near)
+    words = kc.conv3x3_image_lif(img.to(DEV), w.to(DEV), b.to(DEV), T, decay=0.5, in_scale=0.5,
+                                 v_threshold=1.0, out_bits=True).cpu()
+    bits = (words.unsqueeze(-1) >> torch.arange(32)) & 1
+    assert torch.equal(bits.reshape(*words.shape[:-1], Cout).to(torch.bfloat16), spk.cpu())
+
+
 def test_image_layer_and_layout():
     g = torch.Generator().manual_seed(4)
     img = torch.randn(3, 3, 12, 10, generator=g)
